@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""Benchmark of the FP16 blocked-layout tensor path on one MI355X.
+
+One *step* = the per-channel broadcast affine + SiLU workload y = SiLU(x*s + b)
+over NC1HWC0 fp16 tensors at the three YOLOv8s neck shapes (C,H,W) in
+{(128,80,80), (256,40,40), (512,20,20)} with N=32, each run on the full tensor
+and on the C2f half-split narrowed view x[:, C/2:] -- six launches of the
+fused kernel.  ``value`` = algorithmic bytes (each input read once, each output
+written once, 2 B per fp16) of a step / step time, in GB/s, with inputs resident
+in HBM and buffer sets rotated (> 512 MB) so the 256 MB Infinity Cache cannot
+serve them.
+
+Also reported (``ops``): per-op / per-chain µs and GB/s at N=1 (cache-resident
+and rotated) and N=32 for every op built, the roofline of the dominant kernel
+and the PyTorch CPU op sequence timed on the host cores (``cpu_baseline``).
+Only rank 0 prints: one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+os.environ.setdefault("TORCH_DEVICE_BACKEND_AUTOLOAD", "0")
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import torch  # noqa: E402
+
+METRIC = "HBM GB/s (% of peak) + µs/op, YOLOv8s fp16 eltwise/softmax, N=1 & N=32"
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 640 << 20  # > 2x the 256 MB Infinity Cache
+C2_SHAPES = [(128, 80, 80), (256, 40, 40), (512, 20, 20)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ inputs
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def blocked_normal(n, c, h, w, seed, dev, std=1.0, mean=0.0):
+    """NC1HWC0 fp16 [n, c/16, h, w, 16] with N(mean, std) values, made on the GPU
+    from a seeded GPU generator (the parity tests use CPU-seeded inputs; timing
+    only needs the right shapes and value ranges)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return (torch.randn((n, c // 16, h, w, 16), generator=g, device=dev) * std + mean).half()
+
+
+def c2_set(n, c, h, w, dev, seed):
+    x = blocked_normal(n, c, h, w, seed, dev)
+    g = torch.Generator(device=dev).manual_seed(seed + 7)
+    s = (torch.rand((1, c // 16, 1, 1, 16), generator=g, device=dev) + 0.5).half()
+    b = (torch.randn((1, c // 16, 1, 1, 16), generator=g, device=dev) * 0.1).half()
+    y = torch.empty_like(x)
+    return x, s, b, y
+
+
+# ------------------------------------------------------------------ timing
+
+def time_launches(launch, sets, iters, rounds=5):
+    """Median over `rounds` of (event elapsed / iters) for `iters` back-to-back
+    launches cycling through `sets`; HIP events recorded on the stream the
+    kernels are launched on (torch's current stream).  Returns seconds."""
+    stream = torch.cuda.current_stream()
+    for i in range(min(len(sets), 3)):
+        launch(sets[i])
+    torch.cuda.synchronize()
+    res = []
+    for _ in range(rounds):
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(iters):
+            launch(sets[i % len(sets)])
+        stop.record(stream)
+        stop.synchronize()
+        res.append(start.elapsed_time(stop) / 1e3 / iters)
+    return statistics.median(res)
+
+
+def rotation_count(bytes_per_set):
+    return max(2, math.ceil(ROTATE_BYTES / max(1, bytes_per_set)))
+
+
+# ------------------------------------------------------------------ ops
+
+def op_affine_silu(capi, dev, n, c, h, w, narrowed, rotate=True):
+    """Returns (launch, sets, algorithmic bytes)."""
+    c1 = c // 16
+    per = n * c1 * h * w * 16 * 2
+    frac = 0.5 if narrowed else 1.0
+    algo = int(per * frac * 2 + 2 * c1 * 16 * 2 * frac)
+    nsets = rotation_count(per * 2) if rotate else 1
+    sets = [c2_set(n, c, h, w, dev, 11 + i) for i in range(nsets)]
+
+    def launch(st):
+        x, s, b, y = st
+        if narrowed:
+            capi.affine_silu(x[:, c1 // 2:], s[:, c1 // 2:], b[:, c1 // 2:], out=y[:, c1 // 2:])
+        else:
+            capi.affine_silu(x, s, b, out=y)
+    return launch, sets, algo
+
+
+def op_silu_add(capi, dev, n, rotate=True):
+    per = n * 4 * 160 * 160 * 16 * 2
+    nsets = rotation_count(per * 3) if rotate else 1
+    sets = [(blocked_normal(n, 64, 160, 160, 21 + i, dev), blocked_normal(n, 64, 160, 160, 51 + i, dev),
+             torch.empty((n, 4, 160, 160, 16), dtype=torch.float16, device=dev)) for i in range(nsets)]
+
+    def launch(st):
+        capi.silu_add(st[0], st[1], out=st[2])
+    return launch, sets, per * 3
+
+
+def op_rows(capi, dev):
+    """(name, cfg, N, factory) for the per-op table."""
+    rows = []
+    for n in (1, 32):
+        rows.append(("silu_add", "C1", n, lambda r, n=n: op_silu_add(capi, dev, n, r)))
+    for n in (1, 32):
+        for (c, h, w) in C2_SHAPES:
+            for narrowed in (False, True):
+                name = f"affine_silu{'_narrowed' if narrowed else ''}_{c}x{h}x{w}"
+                rows.append((name, "C2", n, lambda r, n=n, c=c, h=h, w=w, nr=narrowed:
+                             op_affine_silu(capi, dev, n, c, h, w, nr, r)))
+    return rows
+
+
+# ------------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(budget_s=20.0):
+    """PyTorch CPU op sequence F.silu(torch.add(torch.mul(x, s), b)) in fp16 on
+    the host cores, on a bounded sample (N=2 of each C2 shape).  GB/s uses the
+    same algorithmic bytes as the GPU figure."""
+    from oracle import elementwise as ew  # the oracle's CPU sequence, timed
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    n = 2
+    total_bytes, total_s = 0, 0.0
+    t_end = time.perf_counter() + budget_s
+    for (c, h, w) in C2_SHAPES:
+        g = gen(3)
+        x = (torch.randn((n, c // 16, h, w, 16), generator=g)).half()
+        s = (torch.rand((1, c // 16, 1, 1, 16), generator=g) + 0.5).half()
+        b = (torch.randn((1, c // 16, 1, 1, 16), generator=g) * 0.1).half()
+        for _ in range(3):
+            ew.affine_silu(x, s, b)
+        samples = []
+        while len(samples) < 20 and (len(samples) < 3 or time.perf_counter() < t_end):
+            t0 = time.perf_counter_ns()
+            ew.affine_silu(x, s, b)
+            samples.append((time.perf_counter_ns() - t0) / 1e9)
+        total_s += statistics.median(samples)
+        total_bytes += x.numel() * 2 * 2
+    cpu = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(total_bytes / total_s / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"F.silu(torch.add(torch.mul(x,s),b)) fp16 on CPU, N={n} of each C2 shape "
+                      f"{C2_SHAPES}, median of <=20 samples after 3 warmups; host CPU: {cpu}"}
+
+
+# ------------------------------------------------------------------ main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
+    ap.add_argument("--iters", type=int, default=200, help="launches per per-op timing round")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of "
+              "this path is a design note, not a measured configuration.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    from thintnpu_amd import capi
+    capi.lib()
+    dev = torch.device("cuda:0")
+    n = 32
+
+    # ---- the step: six affine_silu launches at N=32 with rotated buffer sets
+    work = []
+    for (c, h, w) in C2_SHAPES:
+        for narrowed in (False, True):
+            work.append(op_affine_silu(capi, dev, n, c, h, w, narrowed, rotate=False))
+    step_bytes = sum(a for _, _, a in work)
+    per_set = sum(sum(t.numel() * t.element_size() for t in sets[0]) for _, sets, _ in work)
+    nrot = rotation_count(per_set)
+    rot_sets = [[op_affine_silu(capi, dev, n, c, h, w, nr, rotate=False)[1][0]
+                 for (c, h, w) in C2_SHAPES for nr in (False, True)] for _ in range(nrot)]
+
+    def step(i):
+        sets = rot_sets[i % nrot]
+        for (launch, _, _), st in zip(work, sets):
+            launch(st)
+
+    log(f"step: {len(work)} launches, {step_bytes / 1e6:.1f} MB algorithmic, {nrot} rotated sets")
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(args.steps):
+        step(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_s = start.elapsed_time(stop) / 1e3 / args.steps
+    value = step_bytes / step_s / 1e9
+    log(f"step {step_s * 1e6:.1f} us  {value:.1f} GB/s  (wall {wall:.3f} s)")
+
+    # ---- roofline of the dominant kernel: affine_silu on the largest shape, N=32
+    launch, sets, algo = op_affine_silu(capi, dev, n, *C2_SHAPES[0], False, rotate=True)
+    dom_s = time_launches(launch, sets, args.iters)
+    achieved = algo / dom_s / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "map_vec_kernel<_Float16,8,3,4,OpAffineSilu> (thin_affine_silu)",
+                "launch": f"N=32 C,H,W={C2_SHAPES[0]}: {algo} algorithmic bytes, avg {dom_s * 1e6:.2f} us"}
+    del sets
+
+    ops = []
+    if not args.no_ops:
+        for name, cfg, nn, factory in op_rows(capi, dev):
+            for rotate in ((False, True) if nn == 1 else (True,)):
+                launch, sets, algo = factory(rotate)
+                t = time_launches(launch, sets, args.iters)
+                gbs = algo / t / 1e9
+                ops.append({"op": name, "cfg": cfg, "N": nn, "us": round(t * 1e6, 3),
+                            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+                            "bytes": algo, "cache": "rotated" if rotate else "resident"})
+                log(f"{cfg} {name:32s} N={nn:2d} {'rot' if rotate else 'res'} "
+                    f"{t * 1e6:9.2f} us {gbs:8.1f} GB/s")
+                del sets
+                torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "affine+SiLU y=SiLU(x*s+b), per-channel [1,C,1,1] broadcast, NC1HWC0 fp16, "
+                               "N=32, (C,H,W) in {(128,80,80),(256,40,40),(512,20,20)}, full + C2f "
+                               "narrowed view x[:,C/2:]",
+                   "batch": n, "shapes": C2_SHAPES, "launches_per_step": len(work),
+                   "algorithmic_bytes_per_step": step_bytes, "rotated_sets": nrot},
+        "pct_peak": round(100 * value / HBM_PEAK_GBS, 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "ops": ops,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,221 @@
+/*
+ * thin_hip.h -- C ABI of the MI355X (gfx950) FP16 blocked-layout tensor library.
+ *
+ * Every entry point takes plain pointers, sizes and a hipStream_t; no torch
+ * types cross this boundary.  Tensors are described by `thin_desc`: a data
+ * pointer that already includes the storage offset, a dtype, a rank and
+ * per-dimension sizes/strides counted in elements (stride 0 = broadcast).
+ *
+ * Rules shared by every entry point:
+ *   - the library never allocates device memory and never synchronizes; work
+ *     is enqueued on the given stream, so every call is safe to record into a
+ *     HIP graph (hipStreamBeginCapture .. hipStreamEndCapture);
+ *   - a call that cannot run returns a non-zero thin_status and leaves a
+ *     message in thin_last_error() (thread-local); nothing is launched then;
+ *   - calls are thread-safe; the library keeps no per-call state.
+ *
+ * Reference interfaces are cited as file:line of the ThinTNPU sources
+ * (AscendC kernels + libtorch host code) whose behaviour each entry replaces.
+ */
+#ifndef THIN_HIP_H
+#define THIN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define THIN_MAX_DIMS 8
+#define THIN_MAX_CAT_INPUTS 64
+
+typedef enum thin_status {
+  THIN_OK = 0,
+  THIN_ERR_INVALID = 1,     /* argument / shape / dtype contract violated */
+  THIN_ERR_UNSUPPORTED = 2, /* well-formed but outside what the library implements */
+  THIN_ERR_HIP = 3,         /* a HIP runtime call failed (launch error etc.) */
+  THIN_ERR_WORKSPACE = 4    /* caller-provided workspace too small */
+} thin_status;
+
+typedef enum thin_dtype {
+  THIN_F16 = 0,
+  THIN_F32 = 1,
+  THIN_I64 = 2,
+  THIN_I32 = 3,
+  THIN_I16 = 4,
+  THIN_U8 = 5,
+  THIN_F64 = 6,
+  THIN_BF16 = 7
+} thin_dtype;
+
+typedef struct thin_desc {
+  void* data;                       /* address of element [0,...,0] */
+  int32_t dtype;                    /* thin_dtype */
+  int32_t rank;                     /* 0..THIN_MAX_DIMS */
+  int64_t sizes[THIN_MAX_DIMS];
+  int64_t strides[THIN_MAX_DIMS];   /* in elements, >= 0 */
+} thin_desc;
+
+/* Binary operation codes; the numbering follows the reference's
+ * elementwise.cpp:104-115 entries (sub=0, mul=1, div=2, add=3). */
+typedef enum thin_binary_op { THIN_SUB = 0, THIN_MUL = 1, THIN_DIV = 2, THIN_ADD = 3 } thin_binary_op;
+
+typedef enum thin_unary_op { THIN_SIGMOID = 0, THIN_SILU = 1 } thin_unary_op;
+
+/* Last error message of the calling thread ("" after a successful call). */
+const char* thin_last_error(void);
+
+/* Library version string, e.g. "thin-hip 0.1 gfx950". */
+const char* thin_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Elementwise                                                         */
+/* ------------------------------------------------------------------ */
+
+/* out = x op (alpha * y) for add/sub, x*y, x/y; fp16 or fp32.
+ * x, y and out share out's sizes (broadcast operands carry stride 0); any
+ * strides.  fp16 math runs in fp32 with one round-to-nearest-even cast, so
+ * add/sub/mul/div with alpha == 1 are correctly rounded fp16 results.
+ * Replaces thin_ops::binary + sub/add/mul/div (ops.cpp:464-497), the packed
+ * binary_impl kernels (elementwise.cpp:6-45) and strided_binary::launch
+ * (strided_binary.h:192-222). */
+thin_status thin_binary(int32_t op, const thin_desc* x, const thin_desc* y,
+                        const thin_desc* out, float alpha, hipStream_t stream);
+
+/* out = x op scalar (scalar_first == 0) or scalar op x (scalar_first != 0),
+ * with the scalar held at fp32 precision, as PyTorch CPU holds a wrapped
+ * Python number.  Replaces the 0-d CPU operand branch of thin_ops::binary
+ * (ops.cpp:466-467). */
+thin_status thin_binary_scalar(int32_t op, const thin_desc* x, double scalar,
+                               int32_t scalar_first, const thin_desc* out,
+                               float alpha, hipStream_t stream);
+
+/* out = sigmoid(x) or silu(x), computed in fp32, one cast; fp16 or fp32; any
+ * strides (out may alias x exactly, for in-place use).
+ * Replaces thin::sigmoid (backend.cpp:226-244; sigmoid.cpp:6-51),
+ * thin_ops::silu_ (ops.cpp:498-512; elementwise.cpp:47-102) and
+ * thin_aten::sigmoid/silu (aten_adapter.cpp:94-105). */
+thin_status thin_unary(int32_t op, const thin_desc* x, const thin_desc* out,
+                       hipStream_t stream);
+
+/* Fused residual: out = y + silu(x) in fp32 with a single rounding (fp16).
+ * No reference counterpart as one op: replaces the chain silu_ (ops.cpp:498)
+ * followed by add.Tensor (ops.cpp:495) of the C2f Bottleneck residual. */
+thin_status thin_silu_add(const thin_desc* x, const thin_desc* y,
+                          const thin_desc* out, hipStream_t stream);
+
+/* Fused per-channel affine + SiLU: out = silu(round16(round16(x*s) + b)),
+ * fp16, reproducing the fp16 roundings of the unfused mul -> add -> silu
+ * chain (ops.cpp:464-497 twice, then elementwise.cpp:47-102) in registers.
+ * s and b carry out's sizes with broadcast strides (e.g. [1,C1,1,1,16] over
+ * an NC1HWC0 x). */
+thin_status thin_affine_silu(const thin_desc* x, const thin_desc* s,
+                             const thin_desc* b, const thin_desc* out,
+                             hipStream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Data movement (bit-exact)                                           */
+/* ------------------------------------------------------------------ */
+
+/* dst = src elementwise bit copy, equal sizes and dtype, any strides.
+ * Replaces materialize::copy / gather_kernel / transpose_kernel
+ * (ops.cpp:85-295) and the device-to-device leg of thin_ops::copy_strided
+ * (ops.cpp:32-78). */
+thin_status thin_copy(const thin_desc* src, const thin_desc* dst, hipStream_t stream);
+
+/* out = cat(inputs, dim) with PyTorch semantics: every input has out's rank,
+ * and out's sizes outside `dim`; inputs may have any strides (0-sized inputs
+ * contribute nothing).  n <= THIN_MAX_CAT_INPUTS.
+ * Replaces thin_ops::cat (ops.cpp:419-462) with concatenate::concat_kernel
+ * (ops.cpp:309-417) and strided_concat::launch (strided_concat.h:1-247). */
+thin_status thin_cat(const thin_desc* inputs, int32_t n, int32_t dim,
+                     const thin_desc* out, hipStream_t stream);
+
+/* Nearest 2x upsample of an NC1HWC0 fp16/fp32 tensor [N,C1,H,W,C0] into
+ * [N,C1,2H,2W,C0] (any N; any strides on N and C1, H/W/C0 dense).
+ * Replaces blocked_flow::upsample (flow_ops.cpp:129-199,233-252). */
+thin_status thin_upsample2x_nc1hwc0(const thin_desc* x, const thin_desc* y,
+                                    hipStream_t stream);
+
+/* Nearest 2x upsample of NCHW [N,C,H,W] into [N,C,2H,2W] (any strides).
+ * Replaces thin::upsample_nearest2d (backend.cpp:269-286; upsample.cpp:5-132). */
+thin_status thin_upsample2x_nchw(const thin_desc* x, const thin_desc* y,
+                                 hipStream_t stream);
+
+/* Fused neck op: out = cat([up2x(x_i) if upsample[i] else x_i ...], dim=1) on
+ * NC1HWC0 tensors, one launch.  No single reference counterpart: replaces
+ * thin_native_flow::upsample (flow_ops.cpp:233-252) followed by aten::cat
+ * (ops.cpp:419-462). */
+thin_status thin_upsample_cat_nc1hwc0(const thin_desc* inputs, const int32_t* upsample,
+                                      int32_t n, const thin_desc* out, hipStream_t stream);
+
+/* NCHW [N,C,H,W] -> NC1HWC0 [N,ceil(C/16),H,W,16]; channels >= C are zero.
+ * Replaces native_flow::pack_input (conv_flow.cpp:406-458) and
+ * thin_blocked::pack (layout_blocked.h:2-55); any N. */
+thin_status thin_pack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_t stream);
+
+/* NC1HWC0 [N,C1,H,W,16] -> NCHW [N,C,H,W] with C <= 16*C1 (drops padding).
+ * Replaces thin_blocked::unpack (layout_blocked.h:57-69); any N. */
+thin_status thin_unpack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Reductions                                                          */
+/* ------------------------------------------------------------------ */
+
+/* out = softmax(x, dim): fp32 max / exp / sum, out = e * (1/sum) (last dim)
+ * or e / sum (other dims); NaN/inf follow PyTorch CPU.  x fp16 or fp32, out
+ * fp16/fp32 (fp16 -> fp32 = half_to_float).  x any strides; out any strides.
+ * Replaces thin_softmax::softmax (softmax_host.cpp:51-89), Softmax<T,U,Last>
+ * (softmax.cpp:6-173) and the DFL fast path DflSoftmax (softmax.cpp:175-271;
+ * softmax_host.cpp:29-50). */
+thin_status thin_softmax(const thin_desc* x, int32_t dim, const thin_desc* out,
+                         hipStream_t stream);
+
+/* Fused DFL: x = box logits [N,4*16,A] (fp16, any strides, bins of side s at
+ * channels 16s..16s+15) -> out [N,4,A] (fp16 or fp32) where
+ * out[n,s,a] = sum_i i * softmax_i(x[n,16s+i,a]).  fp32 throughout, one cast.
+ * Replaces DflSoftmax (softmax.cpp:175-271) followed by the 1x1 arange(16)
+ * convolution of the DFL head (model_optimization.py:20-31,
+ * conv_img.cpp:590-597). */
+thin_status thin_dfl_expect(const thin_desc* x, const thin_desc* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* Detection selection (YOLO26 NMS-free top-K)                         */
+/* ------------------------------------------------------------------ */
+
+/* Optional trace outputs; any pointer may be NULL.  Sizes follow
+ * SELECTION_FLOW.md's stage list: class_max fp16 [B,A], stage1 int64 [B,K],
+ * gathered fp16 [B,K,nc] (class-aware only), top_values fp16 [B,K],
+ * stage2 int64 [B,K] (class-aware only), anchors int64 [B,K],
+ * labels int64 [B,K]; all contiguous. */
+typedef struct thin_select_trace {
+  void* class_max;
+  void* stage1;
+  void* gathered;
+  void* top_values;
+  void* stage2;
+  void* anchors;
+  void* labels;
+} thin_select_trace;
+
+/* Bytes of device workspace thin_detection_select needs for these sizes. */
+size_t thin_detection_select_workspace(int64_t batches, int64_t anchors, int64_t classes,
+                                       int64_t max_det, int32_t agnostic);
+
+/* decoded: fp16 [B,A,4+nc], any non-negative strides.  out: fp32 [B,K,6]
+ * contiguous, K = min(max_det, A); rows (box0..3, score, class).  Order:
+ * ascending (score_key(bits), index) -- NaN first, +-0 equal, lower index
+ * wins ties; class max keeps the first best class.  Bit-exact by contract.
+ * workspace: >= thin_detection_select_workspace(...) bytes, 256-B aligned.
+ * Replaces detection_selection::run / detection_select /
+ * detection_select_trace (selection_flow.cpp:429-499). */
+thin_status thin_detection_select(const thin_desc* decoded, int64_t max_det, int32_t agnostic,
+                                  void* out, void* workspace, size_t workspace_bytes,
+                                  const thin_select_trace* trace, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* THIN_HIP_H */

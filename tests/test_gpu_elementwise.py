@@ -1,0 +1,218 @@
+"""GPU parity of the elementwise entry points (through the C ABI) against the
+CPU oracle.  Bars: add/sub/mul/div bit-exact (correctly rounded), sigmoid /
+SiLU / fused chains <= 2 fp16 ulp; fp32 tensors within 1e-5 relative."""
+import math
+
+import pytest
+import torch
+
+from oracle import elementwise as ew
+from oracle.numerics import assert_ulp, assert_fused_cancel, bits_equal
+from tests.helpers import normal16, random_bits16, specials16, to_blocked, gen
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1,), (3,), (7,), (100,), (2047,), (2048,), (2049,), (16385,), (65537,), (0,), (), (3, 5, 7)]
+
+
+def run_binary(capi, op, a, b, dev, alpha=1.0):
+    return capi.binary(op, a.to(dev), b.to(dev), alpha).cpu()
+
+
+def check(actual, expected, max_ulp, what):
+    if expected.dtype == torch.float16:
+        return assert_ulp(actual, expected, max_ulp, what)
+    torch.testing.assert_close(actual, expected, rtol=1e-5, atol=1e-6, equal_nan=True, msg=what)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_binary_shapes(gpu, dtype):
+    from thintnpu_amd import capi
+    g = gen(42)
+    for shape in SHAPES:
+        a = (torch.rand(shape, generator=g) * 2 - 1).to(dtype)
+        b = (torch.rand(shape, generator=g) + 0.5).to(dtype)
+        for op in (0, 1, 2, 3):
+            check(run_binary(capi, op, a, b, gpu), ew.binary(op, a, b), 0, f"op{op} {shape}")
+    a = torch.rand(2, 5, 7, generator=g).to(dtype)
+    b = (torch.rand(2, 5, 7, generator=g) + 0.5).to(dtype)
+    for op in (0, 1, 2, 3):
+        got = capi.binary(op, a.to(gpu).transpose(0, 2), b.to(gpu).transpose(0, 2)).cpu()
+        check(got, ew.binary(op, a.transpose(0, 2), b.transpose(0, 2)), 0, f"transposed op{op}")
+    for op in (0, 3):
+        for alpha in (2.0, 0.3):
+            check(run_binary(capi, op, a, b, gpu, alpha), ew.binary(op, a, b, alpha), 0, f"alpha {alpha}")
+
+
+def test_binary_all_encodings_bit_exact(gpu):
+    from thintnpu_amd import capi
+    a = torch.cat([random_bits16((1 << 20,), 1), specials16().repeat_interleave(16)])
+    b = torch.cat([random_bits16((1 << 20,), 2), specials16().repeat(16)])
+    for op in (0, 1, 2, 3):
+        assert_ulp(run_binary(capi, op, a, b, gpu), ew.binary(op, a, b), 0, f"op{op} encodings")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_strided_broadcast_cases(gpu, dtype):
+    """The case list of the reference's strided-binary test (verify_strided_binary.py:24-33)."""
+    from thintnpu_amd import capi
+    g = gen(71)
+    for width in (16, 48, 2048, 2064, 8400):
+        data = torch.randn(4, width * 2 + 16, generator=g).to(dtype)
+        full = torch.randn(4, width, generator=g).to(dtype)
+        scalar = torch.tensor(2, dtype=dtype)
+        dd, fd, sd = data.to(gpu), full.to(gpu), scalar.to(gpu)
+        cases = [
+            ("interleaved-left", lambda d, f, s: (d[:, 1:1 + 2 * width:2], f)),
+            ("interleaved-right", lambda d, f, s: (f, d[:, :2 * width:2])),
+            ("unaligned", lambda d, f, s: (d[:, 1:1 + width], f)),
+            ("row-broadcast", lambda d, f, s: (f, f[:1])),
+            ("column-broadcast", lambda d, f, s: (f, f[:, :1])),
+            ("scalar", lambda d, f, s: (f, s)),
+            ("both-expanded", lambda d, f, s: (f[:1], f[:, :1])),
+            ("rank-four", lambda d, f, s: (f.view(2, 2, 1, width), d[:, :2 * width:2].view(2, 2, 1, width))),
+        ]
+        for label, make in cases:
+            xc, yc = make(data, full, scalar)
+            xg, yg = make(dd, fd, sd)
+            for op in (0, 1, 2, 3):
+                for alpha in ((1.0, 0.3) if op in (0, 3) else (1.0,)):
+                    got = capi.binary(op, xg, yg, alpha).cpu()
+                    check(got, ew.binary(op, xc, yc, alpha), 0, f"{label} w{width} op{op} a{alpha}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_narrowed_blocked_views(gpu, dtype):
+    """Channel-lane slices of 5-D NC1HWC0 tensors (verify_narrow_binary.py:24-69)."""
+    from thintnpu_amd import capi
+    g = gen(2931)
+    for h, w in ((80, 80), (44, 76), (20, 20), (1, 16), (1, 2064)):
+        full = torch.randn(1, 3, h, w, 16, generator=g).to(dtype)
+        grid = torch.randn(h, w, 2, generator=g).to(dtype)
+        anchors = torch.randn(1, 3, 1, 1, 2, generator=g).to(dtype)
+        contiguous = torch.randn(1, 3, h, w, 2, generator=g).to(dtype)
+        scalar = torch.tensor(2, dtype=dtype)
+        cpu = dict(full=full, grid=grid, anchors=anchors, contiguous=contiguous, scalar=scalar)
+        dev = {k: v.to(gpu) for k, v in cpu.items()}
+        cases = {
+            "slice-scalar": lambda t: (t["full"][..., :2], t["scalar"]),
+            "offset-slice-scalar": lambda t: (t["full"][..., 2:4], t["scalar"]),
+            "grid": lambda t: (t["contiguous"], t["grid"]),
+            "anchors": lambda t: (t["contiguous"], t["anchors"]),
+            "narrow-both": lambda t: (t["full"][..., :2], t["full"][..., 2:4]),
+            "narrow-swapped": lambda t: (t["scalar"], t["full"][..., 2:4]),
+            "narrow-broadcast": lambda t: (t["full"][:, :1, ..., :2], t["full"][..., :1]),
+            "lanes-four": lambda t: (t["full"][..., 1:5], t["scalar"]),
+            "lanes-eight": lambda t: (t["full"][..., 1:9], t["scalar"]),
+        }
+        for label, make in cases.items():
+            xc, yc = make(cpu)
+            xg, yg = make(dev)
+            for op in (0, 1, 2, 3):
+                got = capi.binary(op, xg, yg).cpu()
+                check(got, ew.binary(op, xc, yc), 0, f"{label} {h}x{w} op{op}")
+
+
+def test_scalar_operands(gpu):
+    from thintnpu_amd import capi
+    x = torch.cat([random_bits16((100_000,), 5), specials16()])
+    xg = x.to(gpu)
+    for sc in (0.17677669529663687, 0.5, 3.0, -7.25):
+        for op in (0, 1, 2, 3):
+            for first in ((False, True) if op in (0, 3) else (False,)):
+                got = capi.binary_scalar(op, xg, sc, first).cpu()
+                assert_ulp(got, ew.binary_scalar(op, x, sc, first), 0, f"scalar {sc} op{op} first{first}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_unary(gpu, dtype):
+    from thintnpu_amd import capi
+    for shape in ((1,), (5000,), (65537,), (0,), (), (2, 7, 5, 7)):
+        n = math.prod(shape)
+        x = torch.linspace(-8, 8, max(1, n))[:n].reshape(shape).to(dtype)
+        for op, ref in ((capi.SIGMOID, ew.sigmoid), (capi.SILU, ew.silu)):
+            check(capi.unary(op, x.to(gpu)).cpu(), ref(x), 2, f"unary{op} {shape}")
+    if dtype == torch.float16:
+        x = torch.cat([random_bits16((1 << 20,), 9), specials16()])
+        for op, ref in ((capi.SIGMOID, ew.sigmoid), (capi.SILU, ew.silu)):
+            rep = assert_ulp(capi.unary(op, x.to(gpu)).cpu(), ref(x), 2, f"unary{op} encodings")
+            assert rep["exact"] > 0.99 * rep["finite"]
+
+
+def test_unary_in_place_on_strided_parent(gpu):
+    """silu_ on a channel split of a parent tensor (verify_ops.py:105-115)."""
+    from thintnpu_amd import capi
+    a = normal16((2, 7, 5, 7), 10)
+    x = a.to(gpu)
+    part = torch.split(x, [3, 4], 1)[1]
+    capi.unary(capi.SILU, part, out=part)
+    ref = a.clone()
+    torch.split(ref, [3, 4], 1)[1].copy_(ew.silu(torch.split(a, [3, 4], 1)[1]))
+    assert_ulp(x.cpu(), ref, 2, "silu_ in place")
+
+
+@pytest.mark.parametrize("n", [1, 32])
+def test_silu_add_c1(gpu, n):
+    """C1: z = y + SiLU(x) on NC1HWC0 [n,4,160,160,16] from NCHW N(0,1), seed 1."""
+    from thintnpu_amd import capi
+    x = to_blocked(normal16((n, 64, 160, 160), 1))
+    y = to_blocked(normal16((n, 64, 160, 160), 101))
+    got = capi.silu_add(x.to(gpu), y.to(gpu)).cpu()
+    # <= 2 fp16 ulp, or <= 4 fp32 ulp of |silu(x)| where y + silu(x) cancels
+    rep = assert_fused_cancel(got, ew.silu_add(x, y), ew.silu(x.float()), 2, 4, f"silu_add n={n}")
+    assert rep["exact"] > 0.999 * rep["finite"]
+
+
+C2_SHAPES = [(128, 80, 80), (256, 40, 40), (512, 20, 20)]
+
+
+def c2_inputs(n, c, h, w, seed=2):
+    x = to_blocked(normal16((n, c, h, w), seed))
+    g = gen(seed + 1000)
+    s = (torch.rand((1, c, 1, 1), generator=g) + 0.5).half()
+    b = (torch.randn((1, c, 1, 1), generator=g) * 0.1).half()
+    return x, to_blocked(s), to_blocked(b)
+
+
+@pytest.mark.parametrize("n", [1, 32])
+@pytest.mark.parametrize("chw", C2_SHAPES)
+def test_affine_silu_c2(gpu, n, chw):
+    """C2: y = SiLU(x*s + b), per-channel [1,C,1,1] broadcast in NC1HWC0, plus the
+    C2f half-split narrowed view x[:, C/2:] (blocked dim-1 offset C/32)."""
+    from thintnpu_amd import capi
+    c, h, w = chw
+    x, s, b = c2_inputs(n, c, h, w)
+    xg, sg, bg = x.to(gpu), s.to(gpu), b.to(gpu)
+    got = capi.affine_silu(xg, sg, bg).cpu()
+    assert_ulp(got, ew.affine_silu(x, s, b), 2, f"affine_silu {n} {chw}")
+    c1 = c // 16
+    xn, sn, bn = x[:, c1 // 2:], s[:, c1 // 2:], b[:, c1 // 2:]
+    got = capi.affine_silu(xg[:, c1 // 2:], sg[:, c1 // 2:], bg[:, c1 // 2:]).cpu()
+    assert_ulp(got, ew.affine_silu(xn, sn, bn), 2, f"affine_silu narrowed {n} {chw}")
+
+
+def test_copy_bit_exact(gpu):
+    from thintnpu_amd import capi
+    raw = random_bits16((3, 32, 48), 913)
+    for view in (lambda t: t.transpose(1, 2), lambda t: t[..., 2:4], lambda t: t[:, ::2, ::2],
+                 lambda t: t[:, :1].expand(-1, 31, -1), lambda t: t):
+        src = view(raw.to(gpu))
+        dst = torch.empty(src.shape, dtype=src.dtype, device=gpu)
+        capi.copy(src, dst)
+        assert bits_equal(dst.cpu(), view(raw).contiguous())
+    for dtype in (torch.float32, torch.int64, torch.uint8):
+        t = torch.arange(3 * 5 * 7).reshape(3, 5, 7).to(dtype)
+        src = t.to(gpu).permute(2, 0, 1)
+        dst = torch.empty(src.shape, dtype=dtype, device=gpu)
+        capi.copy(src, dst)
+        assert torch.equal(dst.cpu(), t.permute(2, 0, 1).contiguous())
+
+
+def test_errors_are_reported(gpu):
+    from thintnpu_amd import capi
+    a = torch.ones(4, device=gpu, dtype=torch.float16)
+    b = torch.ones(4, device=gpu, dtype=torch.float32)
+    with pytest.raises(capi.ThinError, match="matching dtypes"):
+        capi.binary(capi.ADD, a, b)
+    with pytest.raises(capi.ThinError, match="float32/float16"):
+        capi.unary(capi.SILU, torch.ones(4, device=gpu, dtype=torch.int64))

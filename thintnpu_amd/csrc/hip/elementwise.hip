@@ -1,0 +1,485 @@
+// Elementwise kernels: binary (add/sub/mul/div with alpha), scalar binary,
+// sigmoid, SiLU, the fused silu_add / affine_silu chains and strided bit
+// copies.  One grid-stride kernel family serves all of them:
+//
+//   * dimensions of all operands are coalesced on the host (dim 0 innermost
+//     in the kernel plan) and passed by value -- no metadata upload;
+//   * when the innermost coalesced dimension is a multiple of the vector
+//     width V (16 bytes of elements), each thread handles V consecutive
+//     outputs; every operand then loads in one of three modes, chosen per
+//     operand on the host: 16-byte vector (stride 1, aligned), broadcast
+//     (stride 0: one scalar load) or gather (V strided scalar loads);
+//   * otherwise a one-element-per-thread path handles any layout.
+//
+// Arithmetic for fp16 tensors runs in fp32 and rounds once to nearest-even;
+// see the per-op notes for the reference behaviour each one matches.
+#include "common.h"
+
+#include <string.h>
+
+namespace thin {
+namespace {
+
+using dev::fast_exp_neg;
+using dev::fast_rcp;
+
+constexpr uint32_t kThreads = 256;
+
+enum LoadMode : uint32_t { kVec = 0, kBcast = 1, kGather = 2 };
+
+// Offsets are 32-bit: the host splits a launch into slabs whose element
+// spans fit in int32 for every operand.
+template <int NIN>
+struct MapPlan {
+  int32_t nd;                       // coalesced dims, index 0 innermost
+  uint32_t size[kMaxDims];
+  FastDiv div[kMaxDims];
+  int32_t ostride[kMaxDims];
+  int32_t istride[NIN][kMaxDims];
+  void* out;
+  const void* in[NIN];
+  uint32_t units;                   // vectors (V > 1) or elements (V == 1)
+  uint32_t in_mode[NIN];            // LoadMode per input (V > 1 only)
+  uint32_t out_mode;                // kVec or kGather (V > 1 only)
+  float pa, pb;                     // op parameters (alpha, scalar)
+};
+
+// ------------------------------------------------------------ op functors
+// Each functor maps NIN storage values of type T to one T.
+
+template <typename T> __device__ __forceinline__ float to_f(T v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v; }
+
+// Sigmoid / SiLU.  fp16: fp32 evaluation through the hardware exp2 and
+// reciprocal (a few fp32 ulps, far below one fp16 ulp); fp32: library expf and
+// IEEE division, as PyTorch CPU's 1/(1+exp(-x)) and x/(1+exp(-x))
+// (sigmoid.cpp:30-36 and elementwise.cpp:76-86 compute the same formulas).
+template <typename T> __device__ __forceinline__ float sigmoid_f(float x);
+template <> __device__ __forceinline__ float sigmoid_f<_Float16>(float x) {
+  return fast_rcp(1.0f + fast_exp_neg(x));
+}
+template <> __device__ __forceinline__ float sigmoid_f<float>(float x) {
+  return 1.0f / (1.0f + expf(-x));
+}
+template <typename T> __device__ __forceinline__ float silu_f(float x);
+template <> __device__ __forceinline__ float silu_f<_Float16>(float x) {
+  return x * fast_rcp(1.0f + fast_exp_neg(x));
+}
+template <> __device__ __forceinline__ float silu_f<float>(float x) {
+  return x / (1.0f + expf(-x));
+}
+
+struct OpCopy {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const { return v[0]; }
+};
+// x + alpha*y as one fp32 fused multiply-add: with alpha == 1 this is the
+// correctly rounded sum, and fp32 -> fp16 double rounding is innocuous for
+// fp16 operands (24 >= 2*11 + 2).
+struct OpAdd {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float alpha, float) const {
+    return from_f<T>(fmaf(alpha, to_f(v[1]), to_f(v[0])));
+  }
+};
+struct OpSub {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float alpha, float) const {
+    return from_f<T>(fmaf(-alpha, to_f(v[1]), to_f(v[0])));
+  }
+};
+struct OpMul {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const {
+    return from_f<T>(to_f(v[0]) * to_f(v[1]));
+  }
+};
+struct OpDiv {  // IEEE fp32 division (hipcc's default correctly rounded divide)
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const {
+    return from_f<T>(to_f(v[0]) / to_f(v[1]));
+  }
+};
+// Tensor (op) fp32 scalar; `pb` holds the scalar.  SUB/ADD use alpha on the
+// scalar operand exactly as the Tensor-Tensor forms do.
+template <int OP, bool SCALAR_FIRST>
+struct OpScalar {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float alpha, float s) const {
+    float x = to_f(v[0]);
+    float a = SCALAR_FIRST ? s : x;
+    float b = SCALAR_FIRST ? x : s;
+    float r;
+    if (OP == THIN_ADD) r = fmaf(alpha, b, a);
+    else if (OP == THIN_SUB) r = fmaf(-alpha, b, a);
+    else if (OP == THIN_MUL) r = a * b;
+    else r = a / b;
+    return from_f<T>(r);
+  }
+};
+struct OpSigmoid {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const {
+    return from_f<T>(sigmoid_f<T>(to_f(v[0])));
+  }
+};
+struct OpSilu {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const {
+    return from_f<T>(silu_f<T>(to_f(v[0])));
+  }
+};
+// y + silu(x), one rounding.  The residual add can cancel (y ~ -silu(x)), which
+// magnifies any fp32 error of silu(x) relative to the small result, so this op
+// evaluates silu with the library expf and IEEE division -- the same formula and
+// accuracy class as PyTorch CPU's fp32 x / (1 + exp(-x)).
+struct OpSiluAdd {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const {
+    float x = to_f(v[0]);
+    return from_f<T>(to_f(v[1]) + x / (1.0f + expf(-x)));
+  }
+};
+// silu(round(round(x*s) + b)): the fp16 roundings of the unfused chain.
+struct OpAffineSilu {
+  template <typename T, int NIN>
+  __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const {
+    T t1 = from_f<T>(to_f(v[0]) * to_f(v[1]));
+    T t2 = from_f<T>(to_f(t1) + to_f(v[2]));
+    return from_f<T>(silu_f<T>(to_f(t2)));
+  }
+};
+
+// ------------------------------------------------------------ kernels
+
+template <typename T, int V>
+struct alignas(16) VecT {
+  T v[V];
+};
+
+template <typename T, int V, int NIN, int ND, class Op>
+__global__ __launch_bounds__(kThreads) void map_vec_kernel(MapPlan<NIN> p) {
+  const uint32_t step = gridDim.x * kThreads;
+  for (uint32_t u = blockIdx.x * kThreads + threadIdx.x; u < p.units; u += step) {
+    uint32_t e = u * (uint32_t)V;
+    int32_t oo = 0;
+    int32_t io[NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) io[k] = 0;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      if (d >= p.nd) break;
+      uint32_t q = p.div[d].div(e);
+      int32_t c = (int32_t)(e - q * p.size[d]);
+      e = q;
+      oo += c * p.ostride[d];
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) io[k] += c * p.istride[k][d];
+    }
+    T val[V][NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) {
+      const T* src = static_cast<const T*>(p.in[k]) + io[k];
+      if (p.in_mode[k] == kVec) {
+        VecT<T, V> w = *reinterpret_cast<const VecT<T, V>*>(src);
+#pragma unroll
+        for (int j = 0; j < V; ++j) val[j][k] = w.v[j];
+      } else if (p.in_mode[k] == kBcast) {
+        T s = *src;
+#pragma unroll
+        for (int j = 0; j < V; ++j) val[j][k] = s;
+      } else {
+        const int32_t st = p.istride[k][0];
+#pragma unroll
+        for (int j = 0; j < V; ++j) val[j][k] = src[j * st];
+      }
+    }
+    VecT<T, V> r;
+    const Op op;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      T lane[NIN];
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) lane[k] = val[j][k];
+      r.v[j] = op.template operator()<T, NIN>(lane, p.pa, p.pb);
+    }
+    T* dst = static_cast<T*>(p.out) + oo;
+    if (p.out_mode == kVec) {
+      *reinterpret_cast<VecT<T, V>*>(dst) = r;
+    } else {
+      const int32_t st = p.ostride[0];
+#pragma unroll
+      for (int j = 0; j < V; ++j) dst[j * st] = r.v[j];
+    }
+  }
+}
+
+template <typename T, int NIN, int ND, class Op>
+__global__ __launch_bounds__(kThreads) void map_scalar_kernel(MapPlan<NIN> p) {
+  const uint32_t step = gridDim.x * kThreads;
+  for (uint32_t u = blockIdx.x * kThreads + threadIdx.x; u < p.units; u += step) {
+    uint32_t e = u;
+    int32_t oo = 0;
+    int32_t io[NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) io[k] = 0;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      if (d >= p.nd) break;
+      uint32_t q = p.div[d].div(e);
+      int32_t c = (int32_t)(e - q * p.size[d]);
+      e = q;
+      oo += c * p.ostride[d];
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) io[k] += c * p.istride[k][d];
+    }
+    T lane[NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) lane[k] = static_cast<const T*>(p.in[k])[io[k]];
+    const Op op;
+    static_cast<T*>(p.out)[oo] = op.template operator()<T, NIN>(lane, p.pa, p.pb);
+  }
+}
+
+// ------------------------------------------------------------ host launcher
+
+// Elements addressable by one launch (32-bit unit decomposition and offsets).
+constexpr int64_t kSpanLimit = ((int64_t)1 << 31) - 1;
+
+template <typename T, int NIN, int ND, class Op>
+void launch_plan(const MapPlan<NIN>& p, bool vec, hipStream_t stream) {
+  constexpr int V = 16 / (int)sizeof(T);
+  uint32_t grid = grid_for(p.units, kThreads, 1, 256u * 8u);
+  if (vec)
+    hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, Op>), dim3(grid), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((map_scalar_kernel<T, NIN, ND, Op>), dim3(grid), dim3(kThreads), 0, stream, p);
+}
+
+template <typename T, int NIN, class Op>
+thin_status launch_map(const thin_desc* out, const thin_desc* const* ins, float pa, float pb,
+                       hipStream_t stream) {
+  constexpr int V = 16 / (int)sizeof(T);
+  const thin_desc* ops[kMaxOps];
+  ops[0] = out;
+  for (int k = 0; k < NIN; ++k) ops[k + 1] = ins[k];
+  Coalesced c = coalesce(ops, NIN + 1);
+  // Kernel plan dims are innermost-first.
+  const int nd = c.nd;
+  int64_t size[kMaxDims];
+  int64_t st[kMaxOps][kMaxDims];
+  for (int i = 0; i < nd; ++i) {
+    size[i] = c.size[nd - 1 - i];
+    for (int k = 0; k <= NIN; ++k) st[k][i] = c.stride[k][nd - 1 - i];
+  }
+  // Split the outermost dim into slabs whose element count and per-operand
+  // offset span fit in 31 bits.
+  int64_t inner = 1, inner_span = 0;
+  for (int i = 0; i < nd - 1; ++i) inner *= size[i];
+  for (int k = 0; k <= NIN; ++k) {
+    int64_t span = 0;
+    for (int i = 0; i < nd - 1; ++i) span += (size[i] - 1) * st[k][i];
+    if (span > inner_span) inner_span = span;
+  }
+  int64_t outer_stride = 0;
+  for (int k = 0; k <= NIN; ++k)
+    if (st[k][nd - 1] > outer_stride) outer_stride = st[k][nd - 1];
+  THIN_REQUIRE(inner <= kSpanLimit / 2 && inner_span <= kSpanLimit / 2, THIN_ERR_UNSUPPORTED,
+               "elementwise: inner extent %lld (span %lld) exceeds one launch", (long long)inner,
+               (long long)inner_span);
+  const int64_t outer = size[nd - 1];
+  int64_t per_slab = nd == 1 ? kSpanLimit / 2 : (kSpanLimit / 2) / inner;
+  if (outer_stride > 0) {
+    int64_t by_span = (kSpanLimit - inner_span) / outer_stride;
+    if (by_span < per_slab) per_slab = by_span;
+  }
+  if (per_slab < 1) per_slab = 1;
+  if (nd == 1) per_slab -= per_slab % 16;  // keep slab boundaries vector aligned
+
+  for (int64_t o0 = 0; o0 < outer; o0 += per_slab) {
+    int64_t on = outer - o0 < per_slab ? outer - o0 : per_slab;
+    MapPlan<NIN> p;
+    memset(&p, 0, sizeof p);
+    p.nd = nd;
+    for (int i = 0; i < nd; ++i) {
+      int64_t s = i == nd - 1 ? on : size[i];
+      p.size[i] = (uint32_t)s;
+      p.div[i] = FastDiv::make((uint32_t)s);
+      p.ostride[i] = (int32_t)st[0][i];
+      for (int k = 0; k < NIN; ++k) p.istride[k][i] = (int32_t)st[k + 1][i];
+    }
+    p.out = static_cast<char*>(out->data) + o0 * st[0][nd - 1] * (int64_t)sizeof(T);
+    for (int k = 0; k < NIN; ++k)
+      p.in[k] = static_cast<const char*>(ins[k]->data) + o0 * st[k + 1][nd - 1] * (int64_t)sizeof(T);
+    p.pa = pa;
+    p.pb = pb;
+    const int64_t elems = (nd == 1 ? on : inner * on);
+
+    bool vec = V > 1 && p.size[0] % V == 0;
+    if (vec) {
+      auto aligned = [&](const void* ptr, const int64_t* s) {
+        if (reinterpret_cast<uintptr_t>(ptr) % 16) return false;
+        for (int i = 1; i < nd; ++i)
+          if (s[i] % V) return false;
+        return true;
+      };
+      p.out_mode = (st[0][0] == 1 && aligned(p.out, st[0])) ? kVec : kGather;
+      for (int k = 0; k < NIN; ++k) {
+        if (st[k + 1][0] == 0) p.in_mode[k] = kBcast;
+        else if (st[k + 1][0] == 1 && aligned(p.in[k], st[k + 1])) p.in_mode[k] = kVec;
+        else p.in_mode[k] = kGather;
+      }
+      p.units = (uint32_t)(elems / V);
+    } else {
+      p.units = (uint32_t)elems;
+    }
+    if (nd <= 2) launch_plan<T, NIN, 2, Op>(p, vec, stream);
+    else if (nd <= 4) launch_plan<T, NIN, 4, Op>(p, vec, stream);
+    else launch_plan<T, NIN, kMaxDims, Op>(p, vec, stream);
+    THIN_LAUNCH_CHECK("map");
+  }
+  return THIN_OK;
+}
+
+thin_status check_float_operands(const char* what, const thin_desc* const* ds, int n) {
+  for (int k = 0; k < n; ++k) {
+    THIN_REQUIRE(desc_valid(ds[k]), THIN_ERR_INVALID, "%s: invalid descriptor %d", what, k);
+    THIN_REQUIRE(ds[k]->dtype == THIN_F16 || ds[k]->dtype == THIN_F32, THIN_ERR_INVALID,
+                 "%s supports float32/float16, got %s", what, dtype_name(ds[k]->dtype));
+    THIN_REQUIRE(ds[k]->dtype == ds[0]->dtype, THIN_ERR_INVALID,
+                 "%s requires matching dtypes", what);
+    THIN_REQUIRE(same_sizes(ds[k], ds[0]), THIN_ERR_INVALID,
+                 "%s requires operands expanded to the output shape", what);
+  }
+  return THIN_OK;
+}
+
+// Host-side rounding of an op parameter to the tensor dtype.
+float round_to(int32_t dtype, double v) {
+  return dtype == THIN_F16 ? (float)(_Float16)(float)v : (float)v;
+}
+
+template <class Op, int NIN>
+thin_status dispatch_float(const thin_desc* out, const thin_desc* const* ins, float pa, float pb,
+                           hipStream_t stream) {
+  if (numel(out) == 0) return THIN_OK;
+  if (out->dtype == THIN_F16) return launch_map<_Float16, NIN, Op>(out, ins, pa, pb, stream);
+  return launch_map<float, NIN, Op>(out, ins, pa, pb, stream);
+}
+
+}  // namespace
+
+// Raw bit copy used by the copy/cat/materialize paths.
+thin_status copy_bits(const thin_desc* src, const thin_desc* dst, hipStream_t stream) {
+  const thin_desc* ins[1] = {src};
+  if (numel(dst) == 0) return THIN_OK;
+  switch (dtype_size(dst->dtype)) {
+    case 1: return launch_map<uint8_t, 1, OpCopy>(dst, ins, 0.f, 0.f, stream);
+    case 2: return launch_map<uint16_t, 1, OpCopy>(dst, ins, 0.f, 0.f, stream);
+    case 4: return launch_map<uint32_t, 1, OpCopy>(dst, ins, 0.f, 0.f, stream);
+    case 8: return launch_map<uint64_t, 1, OpCopy>(dst, ins, 0.f, 0.f, stream);
+  }
+  set_error("copy: unsupported dtype");
+  return THIN_ERR_INVALID;
+}
+
+}  // namespace thin
+
+using namespace thin;
+
+extern "C" thin_status thin_binary(int32_t op, const thin_desc* x, const thin_desc* y,
+                                   const thin_desc* out, float alpha, hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(x && y && out, THIN_ERR_INVALID, "binary: null descriptor");
+  const thin_desc* all[3] = {out, x, y};
+  thin_status s = check_float_operands("binary", all, 3);
+  if (s) return s;
+  const thin_desc* ins[2] = {x, y};
+  // PyTorch CPU rounds alpha to the tensor dtype before its fp32 evaluation.
+  const float a = round_to(out->dtype, alpha);
+  switch (op) {
+    case THIN_ADD: return dispatch_float<OpAdd, 2>(out, ins, a, 0.f, stream);
+    case THIN_SUB: return dispatch_float<OpSub, 2>(out, ins, a, 0.f, stream);
+    case THIN_MUL: return dispatch_float<OpMul, 2>(out, ins, 1.f, 0.f, stream);
+    case THIN_DIV: return dispatch_float<OpDiv, 2>(out, ins, 1.f, 0.f, stream);
+  }
+  set_error("binary: unknown op %d", op);
+  return THIN_ERR_INVALID;
+}
+
+extern "C" thin_status thin_binary_scalar(int32_t op, const thin_desc* x, double scalar,
+                                          int32_t scalar_first, const thin_desc* out, float alpha,
+                                          hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(x && out, THIN_ERR_INVALID, "binary_scalar: null descriptor");
+  const thin_desc* all[2] = {out, x};
+  thin_status s = check_float_operands("binary_scalar", all, 2);
+  if (s) return s;
+  const thin_desc* ins[1] = {x};
+  // PyTorch CPU semantics of a wrapped Python number on a reduced-precision
+  // tensor: add/sub round the scalar (and alpha) to the tensor dtype, mul/div
+  // keep it at fp32 opmath precision.
+  const bool additive = op == THIN_ADD || op == THIN_SUB;
+  const float sv = additive ? round_to(out->dtype, scalar) : (float)scalar;
+  alpha = round_to(out->dtype, alpha);
+#define THIN_SCALAR_CASE(OPC)                                                              \
+  case OPC:                                                                                \
+    return scalar_first ? dispatch_float<OpScalar<OPC, true>, 1>(out, ins, alpha, sv, stream) \
+                        : dispatch_float<OpScalar<OPC, false>, 1>(out, ins, alpha, sv, stream);
+  switch (op) {
+    THIN_SCALAR_CASE(THIN_ADD)
+    THIN_SCALAR_CASE(THIN_SUB)
+    THIN_SCALAR_CASE(THIN_MUL)
+    THIN_SCALAR_CASE(THIN_DIV)
+  }
+#undef THIN_SCALAR_CASE
+  set_error("binary_scalar: unknown op %d", op);
+  return THIN_ERR_INVALID;
+}
+
+extern "C" thin_status thin_unary(int32_t op, const thin_desc* x, const thin_desc* out,
+                                  hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(x && out, THIN_ERR_INVALID, "unary: null descriptor");
+  const thin_desc* all[2] = {out, x};
+  thin_status s = check_float_operands("unary", all, 2);
+  if (s) return s;
+  const thin_desc* ins[1] = {x};
+  switch (op) {
+    case THIN_SIGMOID: return dispatch_float<OpSigmoid, 1>(out, ins, 0.f, 0.f, stream);
+    case THIN_SILU: return dispatch_float<OpSilu, 1>(out, ins, 0.f, 0.f, stream);
+  }
+  set_error("unary: unknown op %d", op);
+  return THIN_ERR_INVALID;
+}
+
+extern "C" thin_status thin_silu_add(const thin_desc* x, const thin_desc* y, const thin_desc* out,
+                                     hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(x && y && out, THIN_ERR_INVALID, "silu_add: null descriptor");
+  const thin_desc* all[3] = {out, x, y};
+  thin_status s = check_float_operands("silu_add", all, 3);
+  if (s) return s;
+  const thin_desc* ins[2] = {x, y};
+  return dispatch_float<OpSiluAdd, 2>(out, ins, 0.f, 0.f, stream);
+}
+
+extern "C" thin_status thin_affine_silu(const thin_desc* x, const thin_desc* sc, const thin_desc* b,
+                                        const thin_desc* out, hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(x && sc && b && out, THIN_ERR_INVALID, "affine_silu: null descriptor");
+  const thin_desc* all[4] = {out, x, sc, b};
+  thin_status s = check_float_operands("affine_silu", all, 4);
+  if (s) return s;
+  const thin_desc* ins[3] = {x, sc, b};
+  return dispatch_float<OpAffineSilu, 3>(out, ins, 0.f, 0.f, stream);
+}
+
+extern "C" thin_status thin_copy(const thin_desc* src, const thin_desc* dst, hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(desc_valid(src) && desc_valid(dst), THIN_ERR_INVALID, "copy: invalid descriptor");
+  THIN_REQUIRE(same_sizes(src, dst), THIN_ERR_INVALID, "copy requires matching sizes");
+  THIN_REQUIRE(dtype_size(src->dtype) == dtype_size(dst->dtype) && src->dtype == dst->dtype,
+               THIN_ERR_INVALID, "copy requires matching dtypes");
+  return copy_bits(src, dst, stream);
+}
