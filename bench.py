@@ -67,24 +67,37 @@ def c2_set(n, c, h, w, dev, seed):
 
 # ------------------------------------------------------------------ timing
 
+def capture(fn):
+    """Record fn()'s launches (enqueued on torch's current stream, which the
+    C-ABI wrappers use) into a HIP graph via torch's graph capture."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
 def time_launches(launch, sets, iters, rounds=5):
-    """Median over `rounds` of (event elapsed / iters) for `iters` back-to-back
-    launches cycling through `sets`; HIP events recorded on the stream the
-    kernels are launched on (torch's current stream).  Returns seconds."""
-    stream = torch.cuda.current_stream()
+    """Median over `rounds` of (event elapsed / iters) for one replay of a HIP
+    graph holding `iters` back-to-back launches cycling through `sets` (graph
+    replay removes host launch cost, so this is device time per launch).  HIP
+    events are recorded on the stream that replays the graph.  Seconds."""
     for i in range(min(len(sets), 3)):
         launch(sets[i])
+    torch.cuda.synchronize()
+    g = capture(lambda: [launch(sets[i % len(sets)]) for i in range(iters)])
+    stream = torch.cuda.current_stream()
+    g.replay()
     torch.cuda.synchronize()
     res = []
     for _ in range(rounds):
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for i in range(iters):
-            launch(sets[i % len(sets)])
+        g.replay()
         stop.record(stream)
         stop.synchronize()
         res.append(start.elapsed_time(stop) / 1e3 / iters)
+    del g
     return statistics.median(res)
 
 
@@ -187,6 +200,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
     ap.add_argument("--iters", type=int, default=200, help="launches per per-op timing round")
+    ap.add_argument("--profile", action="store_true",
+                    help="only replay the dominant kernel (for rocprofv3 summaries); prints its timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of "
@@ -199,6 +214,12 @@ def main():
     capi.lib()
     dev = torch.device("cuda:0")
     n = 32
+    if args.profile:
+        launch, sets, algo = op_affine_silu(capi, dev, n, *C2_SHAPES[0], False, rotate=True)
+        t = time_launches(launch, sets, args.iters)
+        print(json.dumps({"profile": "affine_silu N=32 C,H,W=(128,80,80)", "us": round(t * 1e6, 3),
+                          "GB/s": round(algo / t / 1e9, 1), "launches": args.iters * 6 + 3}))
+        return
 
     # ---- the step: six affine_silu launches at N=32 with rotated buffer sets
     work = []
@@ -211,10 +232,17 @@ def main():
     rot_sets = [[op_affine_silu(capi, dev, n, c, h, w, nr, rotate=False)[1][0]
                  for (c, h, w) in C2_SHAPES for nr in (False, True)] for _ in range(nrot)]
 
-    def step(i):
-        sets = rot_sets[i % nrot]
+    def step_launches(sets):
         for (launch, _, _), st in zip(work, sets):
             launch(st)
+
+    for sets in rot_sets:  # eager warm pass, then one HIP graph per rotated set
+        step_launches(sets)
+    torch.cuda.synchronize()
+    graphs = [capture(lambda sets=sets: step_launches(sets)) for sets in rot_sets]
+
+    def step(i):
+        graphs[i % nrot].replay()
 
     log(f"step: {len(work)} launches, {step_bytes / 1e6:.1f} MB algorithmic, {nrot} rotated sets")
     for i in range(args.warmup):

@@ -1,0 +1,173 @@
+"""GPU parity of the data-movement entry points (through the C ABI): all
+bit-exact against the CPU oracle, NaN payloads included."""
+import pytest
+import torch
+
+from oracle import movement as mv
+from oracle.numerics import bits_equal
+from tests.helpers import gen, normal16, random_bits16, to_blocked
+
+pytestmark = pytest.mark.gpu
+
+
+def rand_dtype(shape, dtype, seed):
+    g = gen(seed)
+    if dtype == torch.float16:
+        return torch.randint(-32768, 32768, shape, dtype=torch.int16, generator=g).view(torch.float16)
+    return torch.randint(-2 ** 31, 2 ** 31 - 1, shape, dtype=torch.int32, generator=g).view(torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_cat_reference_cases(gpu, dtype):
+    """verify_cat.py:20-54 restated."""
+    from thintnpu_amd import capi
+    seed = 0
+    for dim in range(4):
+        for outer in (1, 3):
+            shape = [outer, 3, 32, 32]
+            parts = []
+            for size in (1, 2, 5):
+                cur = shape.copy()
+                cur[dim] = size if dim != 3 else size * 32
+                seed += 1
+                parts.append(rand_dtype(tuple(cur), dtype, seed))
+            got = capi.cat([p.to(gpu) for p in parts], dim).cpu()
+            assert bits_equal(got, mv.cat(parts, dim)), (dim, outer)
+    for length in (16, 8192, 16384, 16384 + 16, 131072 + 16):
+        parts = [rand_dtype((3, length), dtype, 100 + i) for i in range(3)]
+        assert bits_equal(capi.cat([p.to(gpu) for p in parts], 1).cpu(), mv.cat(parts, 1))
+    for offset in (1, 16):
+        src = rand_dtype((3 * 64 * 64 + offset,), dtype, 7)
+        dev = src.to(gpu)
+        cv, dv = src[offset:].view(3, 64, 64), dev[offset:].view(3, 64, 64)
+        assert bits_equal(capi.cat([dv, dv], 1).cpu(), mv.cat([cv, cv], 1))
+        assert bits_equal(capi.cat([dv.transpose(0, 2)] * 2, 1).cpu(), mv.cat([cv.transpose(0, 2)] * 2, 1))
+    src = rand_dtype((3, 64, 32), dtype, 8)
+    dev = src.to(gpu)
+    assert bits_equal(capi.cat(list(dev.split(32, 1)), 1).cpu(), src)
+    assert bits_equal(capi.cat([dev[:1].expand(3, -1, -1)] * 2, 1).cpu(), mv.cat([src[:1].expand(3, -1, -1)] * 2, 1))
+    shaped_empty = torch.empty(3, 0, 32, dtype=dtype)
+    assert bits_equal(capi.cat([shaped_empty.to(gpu), dev], 1).cpu(), src)
+    assert bits_equal(capi.cat([dev], 1).cpu(), src)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_cat_plan_cases(gpu, dtype):
+    """verify_cat_plan.py:15-52: 1..17 NC1HWC0 inputs, split -> cat round trips."""
+    from thintnpu_amd import capi
+    for count in (1, 2, 3, 4, 6, 8, 9, 17):
+        for batch in (1, 3):
+            for plane in (20, 80):
+                parts = [rand_dtype((batch, 1 + i % 3, plane, plane, 16), dtype, 1000 + i) for i in range(count)]
+                got = capi.cat([p.to(gpu) for p in parts], 1).cpu()
+                assert bits_equal(got, mv.cat(parts, 1)), (count, batch, plane)
+    for rows in (8, 81, 129):
+        parts = [rand_dtype((1, rows, length), dtype, rows + length) for length in (6400, 1600, 400)]
+        assert bits_equal(capi.cat([p.to(gpu) for p in parts], 2).cpu(), mv.cat(parts, 2))
+    for batch in (1, 3):
+        x = rand_dtype((batch, 12, 40, 40, 16), dtype, 5)
+        xd = x.to(gpu)
+        for sizes in ((3, 3, 6), (1, 2, 3, 6)):
+            assert bits_equal(capi.cat(list(xd.split(sizes, 1)), 1).cpu(), x)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_strided_concat_cases(gpu, dtype):
+    """verify_materialize.py:44-74 strided/broadcast/offset concat cases."""
+    from thintnpu_amd import capi
+    for rows in (1, 7, 127, 128, 129, 6400):
+        for widths in ((2, 2, 12), (1, 7, 24), (3, 5, 8), (6, 10)):
+            parts = [rand_dtype((rows, w), dtype, rows * 31 + w) for w in widths]
+            assert bits_equal(capi.cat([p.to(gpu) for p in parts], 1).cpu(), mv.cat(parts, 1))
+    for mode, tr in (("sliced", lambda t: t[::3]), ("broadcast", lambda t: t[:1].expand(273, -1)),
+                     ("offset", lambda t: t[:, 1:])):
+        widths = (2, 2, 12)
+        src = [rand_dtype((273, w + (mode == "offset")), dtype, 77 + w) for w in widths]
+        dev = [tr(s.to(gpu)) for s in src]
+        assert bits_equal(capi.cat(dev, 1).cpu(), mv.cat([tr(s) for s in src], 1)), mode
+
+
+def test_cat_c3_c2f(gpu):
+    """C3: C2f concat of 2+n=4 chunks [N,64,80,80] in NC1HWC0 (two are the halves
+    of one [N,128,80,80] tensor), N in {1,32}."""
+    from thintnpu_amd import capi
+    for n in (1, 32):
+        parent = to_blocked(normal16((n, 128, 80, 80), 3))
+        m1 = to_blocked(normal16((n, 64, 80, 80), 4))
+        m2 = to_blocked(normal16((n, 64, 80, 80), 5))
+        pd = parent.to(gpu)
+        a, b = pd.chunk(2, 1)
+        got = capi.cat([a, b, m1.to(gpu), m2.to(gpu)], 1).cpu()
+        ca, cb = parent.chunk(2, 1)
+        assert bits_equal(got, mv.cat([ca, cb, m1, m2], 1)), n
+
+
+@pytest.mark.parametrize("n", [1, 32])
+def test_upsample_and_fused_cat_c3(gpu, n):
+    """C3: nearest 2x [N,256,40,40] -> [N,256,80,80], then cat with [N,128,80,80];
+    the fused op must equal the two-step composition bit for bit."""
+    from thintnpu_amd import capi
+    x = to_blocked(normal16((n, 256, 40, 40), 6))
+    o = to_blocked(normal16((n, 128, 80, 80), 7))
+    xd, od = x.to(gpu), o.to(gpu)
+    up = capi.upsample2x_nc1hwc0(xd)
+    assert bits_equal(up.cpu(), mv.upsample2x_blocked(x))
+    fused = capi.upsample_cat_nc1hwc0([xd, od], [True, False]).cpu()
+    assert bits_equal(fused, mv.upsample_cat_blocked([x, o], [True, False]))
+    fused2 = capi.upsample_cat_nc1hwc0([od, xd], [False, True]).cpu()
+    assert bits_equal(fused2, mv.upsample_cat_blocked([o, x], [False, True]))
+
+
+def test_upsample_blocked_bit_patterns(gpu):
+    """verify_fast_flow_bits.py:16-22: random int16 patterns, identity of bits."""
+    from thintnpu_amd import capi
+    for c1, h, w in ((16, 20, 20), (32, 20, 20), (16, 40, 40), (8, 40, 40), (2, 13, 17)):
+        for n in (1, 3):
+            x = random_bits16((n, c1, h, w, 16), c1 * h + w + n)
+            assert bits_equal(capi.upsample2x_nc1hwc0(x.to(gpu)).cpu(), mv.upsample2x_blocked(x))
+    # narrowed channel view (any N/C1 strides)
+    x = random_bits16((3, 8, 10, 12, 16), 99)
+    v = x[:, 2:6]
+    assert bits_equal(capi.upsample2x_nc1hwc0(x.to(gpu)[:, 2:6]).cpu(), mv.upsample2x_blocked(v))
+    # a non-dense layout goes through the element map
+    xt = random_bits16((2, 3, 6, 5, 16), 98)
+    vt = xt.transpose(2, 3)
+    assert bits_equal(capi.upsample2x_nc1hwc0(xt.to(gpu).transpose(2, 3)).cpu(), mv.upsample2x_blocked(vt))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_upsample_nchw(gpu, dtype):
+    """verify_all.py:88-94 shapes, atol 0."""
+    from thintnpu_amd import capi
+    for shape in ((1, 2, 5, 7), (2, 3, 13, 11), (1, 64, 40, 40), (2, 4, 6, 8)):
+        x = rand_dtype(shape, dtype, sum(shape))
+        assert bits_equal(capi.upsample2x_nchw(x.to(gpu)).cpu(), mv.upsample2x_nchw(x)), shape
+    x = rand_dtype((2, 14, 15, 17), dtype, 3)
+    sec = x[:, 7:]
+    assert bits_equal(capi.upsample2x_nchw(x.to(gpu)[:, 7:]).cpu(), mv.upsample2x_nchw(sec))
+
+
+def test_pack_unpack(gpu):
+    """C1 repack [1,64,160,160] -> [1,4,160,160,16]; zero pad of a partial C0
+    block (conv_flow.cpp:420); any N; odd planes; non-dense inputs."""
+    from thintnpu_amd import capi
+    for shape in ((1, 64, 160, 160), (2, 3, 16, 16), (3, 17, 13, 17), (32, 64, 20, 20), (1, 40, 7, 9)):
+        x = random_bits16(shape, sum(shape))
+        y = capi.pack_nc1hwc0(x.to(gpu))
+        assert bits_equal(y.cpu(), mv.pack_blocked(x)), shape
+        back = capi.unpack_nc1hwc0(y, shape[1]).cpu()
+        assert bits_equal(back, x), shape
+    x = random_bits16((2, 32, 12, 10), 4)
+    xt = x.transpose(2, 3)
+    assert bits_equal(capi.pack_nc1hwc0(x.to(gpu).transpose(2, 3)).cpu(), mv.pack_blocked(xt))
+
+
+def test_movement_errors(gpu):
+    from thintnpu_amd import capi
+    a = torch.zeros(2, 3, device=gpu, dtype=torch.float16)
+    b = torch.zeros(2, 4, device=gpu, dtype=torch.float32)
+    with pytest.raises(capi.ThinError, match="matching dtypes"):
+        capi.cat([a, b], 1)
+    with pytest.raises(capi.ThinError):
+        capi.upsample_cat_nc1hwc0([torch.zeros(1, 1, 2, 2, 16, device=gpu, dtype=torch.float16)], [False],
+                                  out=torch.zeros(1, 1, 4, 4, 16, device=gpu, dtype=torch.float16))

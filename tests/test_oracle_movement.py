@@ -1,0 +1,65 @@
+"""Pins the data-movement oracle (CPU only)."""
+import itertools
+
+import torch
+import torch.nn.functional as F
+
+from oracle import movement as mv
+from oracle.numerics import bits_equal
+from tests.helpers import random_bits16
+
+
+def test_cat_matches_torch_cat_bits():
+    for dim in range(4):
+        parts = []
+        for i, size in enumerate((1, 2, 5)):
+            shape = [3, 3, 4, 4]
+            shape[dim] = size
+            parts.append(random_bits16(tuple(shape), 10 + i))
+        # torch.cat on int16 views is the library reference for bit movement
+        expect = torch.cat([p.view(torch.int16) for p in parts], dim).view(torch.float16)
+        assert bits_equal(mv.cat(parts, dim), expect)
+    e = torch.empty(0, dtype=torch.float16)
+    x = random_bits16((3, 4), 3)
+    assert bits_equal(mv.cat([e, x, e], 1), x)
+    assert mv.cat([e, e], 0).shape == (0,)
+
+
+def test_upsample_matches_interpolate_and_loops():
+    x = torch.randn(2, 3, 5, 7).half()
+    ref = F.interpolate(x.float(), scale_factor=2, mode="nearest").half()
+    assert bits_equal(mv.upsample2x_nchw(x), ref)
+    xb = random_bits16((2, 3, 4, 5, 16), 4)
+    y = mv.upsample2x_blocked(xb)
+    assert y.shape == (2, 3, 8, 10, 16)
+    yi, xi = y.view(torch.int16), xb.view(torch.int16)
+    for n, c, h, w in itertools.product(range(2), range(3), range(8), range(10)):
+        assert torch.equal(yi[n, c, h, w], xi[n, c, h // 2, w // 2])
+    # a transposed-axis mistake would break the non-square case above; nearest
+    # of the NCHW view of blocked data agrees too
+    nchw = xb.view(torch.int16).permute(0, 1, 4, 2, 3).reshape(2, 48, 4, 5).float()
+    ref = F.interpolate(nchw, scale_factor=2, mode="nearest")
+    got = y.view(torch.int16).permute(0, 1, 4, 2, 3).reshape(2, 48, 8, 10).float()
+    assert torch.equal(got, ref)
+
+
+def test_pack_unpack_brute_force():
+    for c in (3, 16, 17, 40):
+        x = random_bits16((2, c, 3, 5), c)
+        y = mv.pack_blocked(x)
+        c1 = (c + 15) // 16
+        assert y.shape == (2, c1, 3, 5, 16)
+        yi, xi = y.view(torch.int16), x.view(torch.int16)
+        for n, cb, h, w, k in itertools.product(range(2), range(c1), range(3), range(5), range(16)):
+            ch = cb * 16 + k
+            assert yi[n, cb, h, w, k] == (xi[n, ch, h, w] if ch < c else 0)
+        assert bits_equal(mv.unpack_blocked(y, c), x)
+
+
+def test_upsample_cat_composition():
+    a = random_bits16((2, 2, 3, 4, 16), 5)
+    b = random_bits16((2, 1, 6, 8, 16), 6)
+    got = mv.upsample_cat_blocked([a, b], [True, False])
+    assert got.shape == (2, 3, 6, 8, 16)
+    assert bits_equal(got[:, :2], mv.upsample2x_blocked(a))
+    assert bits_equal(got[:, 2:], b)

@@ -157,59 +157,103 @@ struct alignas(16) VecT {
   T v[V];
 };
 
-template <typename T, int V, int NIN, int ND, class Op>
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte store; NT selects a streaming (non-temporal) store for outputs too
+// large to stay cache-resident for their consumer -- on gfx950 it lifts a
+// plain HBM copy from ~5.1 to ~6.6 TB/s.
+template <bool NT, typename W>
+__device__ __forceinline__ void store16(void* dst, const W& w) {
+  static_assert(sizeof(W) == 16, "16-byte store");
+  u32x4 bits = __builtin_bit_cast(u32x4, w);
+  if (NT) __builtin_nontemporal_store(bits, reinterpret_cast<u32x4*>(dst));
+  else *reinterpret_cast<u32x4*>(dst) = bits;
+}
+
+// Output size from which the streaming store is used.
+constexpr int64_t kStreamingStoreBytes = (int64_t)16 << 20;
+
+// Unit offsets for the vector kernel; ND == 1 means every operand is flat
+// (one coalesced dim), so the unit index is the element offset times stride.
+template <int NIN, int ND>
+__device__ __forceinline__ void unit_offsets(const MapPlan<NIN>& p, uint32_t e, int32_t& oo,
+                                             int32_t (&io)[NIN]) {
+  oo = 0;
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) io[k] = 0;
+  if (ND == 1) {
+    oo = (int32_t)e * p.ostride[0];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) io[k] = (int32_t)e * p.istride[k][0];
+    return;
+  }
+#pragma unroll
+  for (int d = 0; d < ND; ++d) {
+    if (d >= p.nd) break;
+    uint32_t q = p.div[d].div(e);
+    int32_t c = (int32_t)(e - q * p.size[d]);
+    e = q;
+    oo += c * p.ostride[d];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) io[k] += c * p.istride[k][d];
+  }
+}
+
+// Each block handles tiles of kThreads*U units; lane t of the block takes
+// units tile + u*kThreads + t, so every load/store instruction of a wave
+// covers 64 consecutive 16-byte vectors when the operand is dense.  All U
+// loads are issued before any math to keep several vectors in flight.
+template <typename T, int V, int NIN, int ND, int U, bool NT, class Op>
 __global__ __launch_bounds__(kThreads) void map_vec_kernel(MapPlan<NIN> p) {
-  const uint32_t step = gridDim.x * kThreads;
-  for (uint32_t u = blockIdx.x * kThreads + threadIdx.x; u < p.units; u += step) {
-    uint32_t e = u * (uint32_t)V;
-    int32_t oo = 0;
-    int32_t io[NIN];
+  const uint32_t tile_units = kThreads * U;
+  for (uint32_t tile = blockIdx.x * tile_units; tile < p.units; tile += gridDim.x * tile_units) {
+    T val[U][V][NIN];
+    int32_t oo[U];
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) io[k] = 0;
+    for (int u = 0; u < U; ++u) {
+      const uint32_t unit = tile + u * kThreads + threadIdx.x;
+      if (unit >= p.units) break;
+      int32_t io[NIN];
+      unit_offsets<NIN, ND>(p, unit * (uint32_t)V, oo[u], io);
 #pragma unroll
-    for (int d = 0; d < ND; ++d) {
-      if (d >= p.nd) break;
-      uint32_t q = p.div[d].div(e);
-      int32_t c = (int32_t)(e - q * p.size[d]);
-      e = q;
-      oo += c * p.ostride[d];
+      for (int k = 0; k < NIN; ++k) {
+        const T* src = static_cast<const T*>(p.in[k]) + io[k];
+        if (p.in_mode[k] == kVec) {
+          VecT<T, V> w = *reinterpret_cast<const VecT<T, V>*>(src);
 #pragma unroll
-      for (int k = 0; k < NIN; ++k) io[k] += c * p.istride[k][d];
-    }
-    T val[V][NIN];
+          for (int j = 0; j < V; ++j) val[u][j][k] = w.v[j];
+        } else if (p.in_mode[k] == kBcast) {
+          T sv = *src;
 #pragma unroll
-    for (int k = 0; k < NIN; ++k) {
-      const T* src = static_cast<const T*>(p.in[k]) + io[k];
-      if (p.in_mode[k] == kVec) {
-        VecT<T, V> w = *reinterpret_cast<const VecT<T, V>*>(src);
+          for (int j = 0; j < V; ++j) val[u][j][k] = sv;
+        } else {
+          const int32_t st = p.istride[k][0];
 #pragma unroll
-        for (int j = 0; j < V; ++j) val[j][k] = w.v[j];
-      } else if (p.in_mode[k] == kBcast) {
-        T s = *src;
-#pragma unroll
-        for (int j = 0; j < V; ++j) val[j][k] = s;
-      } else {
-        const int32_t st = p.istride[k][0];
-#pragma unroll
-        for (int j = 0; j < V; ++j) val[j][k] = src[j * st];
+          for (int j = 0; j < V; ++j) val[u][j][k] = src[j * st];
+        }
       }
     }
-    VecT<T, V> r;
     const Op op;
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      T lane[NIN];
+    for (int u = 0; u < U; ++u) {
+      const uint32_t unit = tile + u * kThreads + threadIdx.x;
+      if (unit >= p.units) break;
+      VecT<T, V> r;
 #pragma unroll
-      for (int k = 0; k < NIN; ++k) lane[k] = val[j][k];
-      r.v[j] = op.template operator()<T, NIN>(lane, p.pa, p.pb);
-    }
-    T* dst = static_cast<T*>(p.out) + oo;
-    if (p.out_mode == kVec) {
-      *reinterpret_cast<VecT<T, V>*>(dst) = r;
-    } else {
-      const int32_t st = p.ostride[0];
+      for (int j = 0; j < V; ++j) {
+        T lane[NIN];
 #pragma unroll
-      for (int j = 0; j < V; ++j) dst[j * st] = r.v[j];
+        for (int k = 0; k < NIN; ++k) lane[k] = val[u][j][k];
+        r.v[j] = op.template operator()<T, NIN>(lane, p.pa, p.pb);
+      }
+      T* dst = static_cast<T*>(p.out) + oo[u];
+      if (p.out_mode == kVec) {
+        store16<NT>(dst, r);
+      } else {
+        const int32_t st = p.ostride[0];
+#pragma unroll
+        for (int j = 0; j < V; ++j) dst[j * st] = r.v[j];
+      }
     }
   }
 }
@@ -218,21 +262,9 @@ template <typename T, int NIN, int ND, class Op>
 __global__ __launch_bounds__(kThreads) void map_scalar_kernel(MapPlan<NIN> p) {
   const uint32_t step = gridDim.x * kThreads;
   for (uint32_t u = blockIdx.x * kThreads + threadIdx.x; u < p.units; u += step) {
-    uint32_t e = u;
-    int32_t oo = 0;
+    int32_t oo;
     int32_t io[NIN];
-#pragma unroll
-    for (int k = 0; k < NIN; ++k) io[k] = 0;
-#pragma unroll
-    for (int d = 0; d < ND; ++d) {
-      if (d >= p.nd) break;
-      uint32_t q = p.div[d].div(e);
-      int32_t c = (int32_t)(e - q * p.size[d]);
-      e = q;
-      oo += c * p.ostride[d];
-#pragma unroll
-      for (int k = 0; k < NIN; ++k) io[k] += c * p.istride[k][d];
-    }
+    unit_offsets<NIN, ND>(p, u, oo, io);
     T lane[NIN];
 #pragma unroll
     for (int k = 0; k < NIN; ++k) lane[k] = static_cast<const T*>(p.in[k])[io[k]];
@@ -241,19 +273,127 @@ __global__ __launch_bounds__(kThreads) void map_scalar_kernel(MapPlan<NIN> p) {
   }
 }
 
+// ------------------------------------------------------------ NC1HWC0 affine
+
+// Per-channel affine + SiLU on NC1HWC0 fp16 planes.  A plane (n, c1) is H*W*16
+// contiguous halves; its 16 scale and 16 bias values are fixed for the whole
+// plane, so each thread keeps the 8 it needs (its C0 half) in registers and
+// the loop body has no index arithmetic beyond one add.  x*s and +b run as
+// packed fp16 multiplies/adds (each correctly rounded, as the unfused fp16
+// chain rounds them); SiLU runs in fp32 and rounds once.
+struct AffinePlan {
+  const _Float16* x;
+  const _Float16* s;
+  const _Float16* b;
+  _Float16* out;
+  int64_t x_n, x_c1, o_n, o_c1, s_n, s_c1, b_n, b_c1;  // element strides
+  uint32_t c1;          // planes per image
+  uint32_t planes;      // N * C1
+  uint32_t plane_vecs;  // H * W * 2 (16-byte vectors per plane)
+};
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+template <int U, bool NT>
+__global__ __launch_bounds__(kThreads) void affine_silu_blocked_kernel(AffinePlan p) {
+  const uint32_t half = threadIdx.x & 1u;  // C0 lanes 0-7 or 8-15
+  for (uint32_t plane = blockIdx.y; plane < p.planes; plane += gridDim.y) {
+    const uint32_t n = plane / p.c1;
+    const uint32_t c1 = plane - n * p.c1;
+    const _Float16* xp = p.x + n * p.x_n + c1 * p.x_c1;
+    _Float16* op = p.out + n * p.o_n + c1 * p.o_c1;
+    const h8v sv = *reinterpret_cast<const h8v*>(p.s + n * p.s_n + c1 * p.s_c1 + half * 8);
+    const h8v bv = *reinterpret_cast<const h8v*>(p.b + n * p.b_n + c1 * p.b_c1 + half * 8);
+    for (uint32_t tile = blockIdx.x * kThreads * U; tile < p.plane_vecs;
+         tile += gridDim.x * kThreads * U) {
+      h8v xv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t v = tile + u * kThreads + threadIdx.x;
+        if (v < p.plane_vecs) xv[u] = *reinterpret_cast<const h8v*>(xp + (size_t)v * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t v = tile + u * kThreads + threadIdx.x;
+        if (v >= p.plane_vecs) break;
+        h8v t = xv[u] * sv;  // packed fp16, correctly rounded
+        t = t + bv;
+        h8v r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = (_Float16)silu_f<_Float16>((float)t[j]);
+        store16<NT>(op + (size_t)v * 8, r);
+      }
+    }
+  }
+}
+
+// Returns true and launches when x/s/b/out have the NC1HWC0 per-channel form.
+bool try_affine_blocked(const thin_desc* x, const thin_desc* sc, const thin_desc* b,
+                        const thin_desc* out, hipStream_t stream) {
+  if (x->dtype != THIN_F16 || x->rank != 5 || x->sizes[4] != 16) return false;
+  const int64_t h = x->sizes[2], w = x->sizes[3];
+  auto dense_plane = [&](const thin_desc* d) {
+    return (h == 1 || d->strides[2] == w * 16) && (w == 1 || d->strides[3] == 16) && d->strides[4] == 1 &&
+           reinterpret_cast<uintptr_t>(d->data) % 16 == 0 && d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0;
+  };
+  auto per_channel = [&](const thin_desc* d) {
+    return d->strides[2] == 0 && d->strides[3] == 0 && d->strides[4] == 1 &&
+           reinterpret_cast<uintptr_t>(d->data) % 16 == 0 && d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0;
+  };
+  if (!dense_plane(x) || !dense_plane(out) || !per_channel(sc) || !per_channel(b)) return false;
+  const int64_t planes = x->sizes[0] * x->sizes[1];
+  const int64_t plane_vecs = h * w * 2;
+  const int64_t span = (x->sizes[0] - 1) * x->strides[0] + (x->sizes[1] - 1) * x->strides[1] + plane_vecs * 8;
+  if (planes >= ((int64_t)1 << 31) || plane_vecs >= ((int64_t)1 << 30) || span >= ((int64_t)1 << 40))
+    return false;
+  AffinePlan p;
+  p.x = static_cast<const _Float16*>(x->data);
+  p.s = static_cast<const _Float16*>(sc->data);
+  p.b = static_cast<const _Float16*>(b->data);
+  p.out = static_cast<_Float16*>(out->data);
+  p.x_n = x->strides[0]; p.x_c1 = x->strides[1];
+  p.o_n = out->strides[0]; p.o_c1 = out->strides[1];
+  p.s_n = sc->strides[0]; p.s_c1 = sc->strides[1];
+  p.b_n = b->strides[0]; p.b_c1 = b->strides[1];
+  p.c1 = (uint32_t)x->sizes[1];
+  p.planes = (uint32_t)planes;
+  p.plane_vecs = (uint32_t)plane_vecs;
+  const uint32_t gy = planes < 65535 ? (uint32_t)planes : 65535u;
+  const bool nt = planes * plane_vecs * 16 >= kStreamingStoreBytes;
+  if (plane_vecs >= 1024) {
+    uint32_t gx = (uint32_t)((plane_vecs + kThreads * 2 - 1) / (kThreads * 2));
+    if (nt) hipLaunchKernelGGL((affine_silu_blocked_kernel<2, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((affine_silu_blocked_kernel<2, false>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+  } else {
+    uint32_t gx = (uint32_t)((plane_vecs + kThreads - 1) / kThreads);
+    if (nt) hipLaunchKernelGGL((affine_silu_blocked_kernel<1, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((affine_silu_blocked_kernel<1, false>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+  }
+  return true;
+}
+
 // ------------------------------------------------------------ host launcher
 
 // Elements addressable by one launch (32-bit unit decomposition and offsets).
 constexpr int64_t kSpanLimit = ((int64_t)1 << 31) - 1;
 
+constexpr int kUnroll = 2;
+
 template <typename T, int NIN, int ND, class Op>
-void launch_plan(const MapPlan<NIN>& p, bool vec, hipStream_t stream) {
+void launch_plan(const MapPlan<NIN>& p, bool vec, bool nt, hipStream_t stream) {
   constexpr int V = 16 / (int)sizeof(T);
-  uint32_t grid = grid_for(p.units, kThreads, 1, 256u * 8u);
-  if (vec)
-    hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, Op>), dim3(grid), dim3(kThreads), 0, stream, p);
-  else
+  if (vec) {
+    uint32_t grid = grid_for(p.units, kThreads, kUnroll, 256u * 64u);
+    if (nt)
+      hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, kUnroll, true, Op>), dim3(grid), dim3(kThreads),
+                         0, stream, p);
+    else
+      hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, kUnroll, false, Op>), dim3(grid), dim3(kThreads),
+                         0, stream, p);
+  } else {
+    uint32_t grid = grid_for(p.units, kThreads, 1, 256u * 16u);
     hipLaunchKernelGGL((map_scalar_kernel<T, NIN, ND, Op>), dim3(grid), dim3(kThreads), 0, stream, p);
+  }
 }
 
 template <typename T, int NIN, class Op>
@@ -333,9 +473,11 @@ thin_status launch_map(const thin_desc* out, const thin_desc* const* ins, float 
     } else {
       p.units = (uint32_t)elems;
     }
-    if (nd <= 2) launch_plan<T, NIN, 2, Op>(p, vec, stream);
-    else if (nd <= 4) launch_plan<T, NIN, 4, Op>(p, vec, stream);
-    else launch_plan<T, NIN, kMaxDims, Op>(p, vec, stream);
+    const bool nt = elems * (int64_t)sizeof(T) >= kStreamingStoreBytes;
+    if (nd == 1) launch_plan<T, NIN, 1, Op>(p, vec, nt, stream);
+    else if (nd <= 2) launch_plan<T, NIN, 2, Op>(p, vec, nt, stream);
+    else if (nd <= 4) launch_plan<T, NIN, 4, Op>(p, vec, nt, stream);
+    else launch_plan<T, NIN, kMaxDims, Op>(p, vec, nt, stream);
     THIN_LAUNCH_CHECK("map");
   }
   return THIN_OK;
@@ -471,6 +613,11 @@ extern "C" thin_status thin_affine_silu(const thin_desc* x, const thin_desc* sc,
   const thin_desc* all[4] = {out, x, sc, b};
   thin_status s = check_float_operands("affine_silu", all, 4);
   if (s) return s;
+  if (numel(out) == 0) return THIN_OK;
+  if (try_affine_blocked(x, sc, b, out, stream)) {
+    THIN_LAUNCH_CHECK("affine_silu_blocked");
+    return THIN_OK;
+  }
   const thin_desc* ins[3] = {x, sc, b};
   return dispatch_float<OpAffineSilu, 3>(out, ins, 0.f, 0.f, stream);
 }

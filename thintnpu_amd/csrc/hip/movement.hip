@@ -1,0 +1,713 @@
+// Data movement, all bit-exact: cat, NC1HWC0 nearest-2x upsample (alone and
+// fused into a channel concat), NCHW nearest-2x upsample, and the
+// NCHW <-> NC1HWC0 (C0 = 16) repack.
+//
+// These kernels are HBM-bound byte movers: 16-byte vector loads/stores wherever
+// the layout allows, streaming stores for large outputs, index math done once
+// per block where it is uniform (plane / input selection), and LDS only for the
+// channel transpose of the repack.
+#include "common.h"
+
+#include <string.h>
+
+namespace thin {
+thin_status copy_bits(const thin_desc* src, const thin_desc* dst, hipStream_t stream);
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+constexpr int64_t kStreamingStoreBytes = (int64_t)16 << 20;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+template <bool NT>
+__device__ __forceinline__ void st16(void* dst, u32x4 v) {
+  if (NT) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));
+  else *reinterpret_cast<u32x4*>(dst) = v;
+}
+__device__ __forceinline__ u32x4 ld16(const void* src) { return *reinterpret_cast<const u32x4*>(src); }
+
+// ============================================================ cat
+
+constexpr int kCatPerLaunch = 16;
+constexpr int kCatOuterDims = THIN_MAX_DIMS - 1;
+
+struct CatPlan {
+  char* out;                         // out row r starts at out + r * out_row (bytes)
+  int64_t out_row;                   // bytes per output row
+  int32_t n_outer;                   // outer dims (before the cat dim)
+  int64_t outer_size[kCatOuterDims];
+  int32_t count;                     // inputs in this launch
+  uint32_t chunks_prefix[kCatPerLaunch + 1];  // block-task prefix over inputs
+  const char* src[kCatPerLaunch];
+  int64_t src_outer_stride[kCatPerLaunch][kCatOuterDims];  // bytes
+  int64_t col_offset[kCatPerLaunch];  // bytes into the output row
+  int64_t run_units[kCatPerLaunch];   // units per row of this input
+  uint32_t chunks_per_row[kCatPerLaunch];
+};
+
+// Units of type W (16-byte vectors or single elements).  A block copies one
+// chunk (kThreads * U units) of one (input, row) run; all index math except
+// the unit offset is uniform per block.
+template <typename W, int U, bool NT>
+__global__ __launch_bounds__(kThreads) void cat_kernel(CatPlan p) {
+  const uint32_t task = blockIdx.x;
+  int i = 0;
+  while (i + 1 < p.count && task >= p.chunks_prefix[i + 1]) ++i;
+  const uint32_t local = task - p.chunks_prefix[i];
+  const uint32_t row = local / p.chunks_per_row[i];
+  const uint32_t chunk = local - row * p.chunks_per_row[i];
+  // row offset of the source: decompose row over the shared outer sizes
+  int64_t src_off = 0;
+  uint64_t r = row;
+  for (int d = p.n_outer - 1; d >= 0; --d) {
+    const uint64_t sz = (uint64_t)p.outer_size[d];
+    const uint64_t c = r % sz;
+    r /= sz;
+    src_off += (int64_t)c * p.src_outer_stride[i][d];
+  }
+  const W* src = reinterpret_cast<const W*>(p.src[i] + src_off);
+  W* dst = reinterpret_cast<W*>(p.out + (int64_t)row * p.out_row + p.col_offset[i]);
+  const int64_t base = (int64_t)chunk * kThreads * U;
+  const int64_t n = p.run_units[i];
+  W v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t k = base + u * kThreads + threadIdx.x;
+    if (k < n) v[u] = src[k];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t k = base + u * kThreads + threadIdx.x;
+    if (k < n) {
+      if constexpr (sizeof(W) == 16) st16<NT>(dst + k, __builtin_bit_cast(u32x4, v[u]));
+      else dst[k] = v[u];
+    }
+  }
+}
+
+// An input whose dims [dim, rank) are dense (row-major, size-1 dims ignored)
+// copies as one run per output row.
+bool run_dense(const thin_desc* t, int dim) {
+  int64_t expect = 1;
+  for (int d = t->rank - 1; d >= dim; --d) {
+    if (t->sizes[d] == 1) continue;
+    if (t->strides[d] != expect) return false;
+    expect *= t->sizes[d];
+  }
+  return true;
+}
+
+template <typename W>
+thin_status launch_cat_group(const thin_desc* const* ins, int count, int dim, const thin_desc* out,
+                             const int64_t* col_elems, int esize, bool nt, hipStream_t stream) {
+  constexpr int U = 4;
+  const int64_t wsize = sizeof(W);
+  CatPlan p;
+  memset(&p, 0, sizeof p);
+  int64_t inner = 1;
+  for (int d = dim + 1; d < out->rank; ++d) inner *= out->sizes[d];
+  int64_t outer = 1;
+  for (int d = 0; d < dim; ++d) outer *= out->sizes[d];
+  p.out = static_cast<char*>(out->data);
+  p.out_row = out->sizes[dim] * inner * esize;
+  p.n_outer = dim;
+  for (int d = 0; d < dim; ++d) p.outer_size[d] = out->sizes[d];
+  p.count = count;
+  uint64_t total = 0;
+  for (int k = 0; k < count; ++k) {
+    const thin_desc* t = ins[k];
+    p.src[k] = static_cast<const char*>(t->data);
+    for (int d = 0; d < dim; ++d) p.src_outer_stride[k][d] = t->strides[d] * esize;
+    p.col_offset[k] = col_elems[k] * esize;
+    const int64_t run_bytes = t->sizes[dim] * inner * esize;
+    p.run_units[k] = run_bytes / wsize;
+    const int64_t cpr = (p.run_units[k] + kThreads * U - 1) / (kThreads * U);
+    p.chunks_per_row[k] = (uint32_t)cpr;
+    p.chunks_prefix[k] = (uint32_t)total;
+    total += (uint64_t)cpr * (uint64_t)outer;
+  }
+  p.chunks_prefix[count] = (uint32_t)total;
+  THIN_REQUIRE(total < (1ull << 31), THIN_ERR_UNSUPPORTED, "cat: too many row chunks (%llu)",
+               (unsigned long long)total);
+  if (total == 0) return THIN_OK;
+  if (nt && wsize == 16)
+    hipLaunchKernelGGL((cat_kernel<W, U, true>), dim3((uint32_t)total), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((cat_kernel<W, U, false>), dim3((uint32_t)total), dim3(kThreads), 0, stream, p);
+  THIN_LAUNCH_CHECK("cat");
+  return THIN_OK;
+}
+
+// ============================================================ NC1HWC0 planes
+
+// Output plane (n, c1) of an NC1HWC0 tensor is either a copy of an input plane
+// or the nearest-2x upsample of one.  Plane = H*W*C0 dense elements; a pixel is
+// `vpp` 16-byte vectors (C0 * element size / 16).
+constexpr int kPlaneInputs = 16;
+struct PlanePlan {
+  char* out;
+  int64_t out_n, out_c1;       // bytes
+  uint32_t out_c1_total;       // C1 of the output
+  uint32_t oh, ow;             // output H, W
+  uint32_t vpp;                // 16-byte vectors per pixel
+  uint32_t plane_vecs;         // oh * ow * vpp
+  int32_t count;
+  uint32_t c1_prefix[kPlaneInputs + 1];
+  const char* src[kPlaneInputs];
+  int64_t src_n[kPlaneInputs], src_c1[kPlaneInputs];  // bytes
+  uint32_t up[kPlaneInputs];   // 1 = upsample 2x
+  uint32_t planes;             // N * out_c1_total
+  FastDiv div_row;             // ow * vpp (vectors per output row)
+  FastDiv div_vpp;
+};
+
+template <int U, bool NT>
+__global__ __launch_bounds__(kThreads) void plane_kernel(PlanePlan p) {
+  for (uint32_t plane = blockIdx.y; plane < p.planes; plane += gridDim.y) {
+    const uint32_t n = plane / p.out_c1_total;
+    const uint32_t c1 = plane - n * p.out_c1_total;
+    int i = 0;
+    while (i + 1 < p.count && c1 >= p.c1_prefix[i + 1]) ++i;
+    const uint32_t ic1 = c1 - p.c1_prefix[i];
+    const char* src = p.src[i] + (int64_t)n * p.src_n[i] + (int64_t)ic1 * p.src_c1[i];
+    char* dst = p.out + (int64_t)n * p.out_n + (int64_t)c1 * p.out_c1;
+    const bool up = p.up[i] != 0;
+    const uint32_t in_row = (p.ow >> 1) * p.vpp;  // vectors per input row (upsample)
+    for (uint32_t tile = blockIdx.x * kThreads * U; tile < p.plane_vecs; tile += gridDim.x * kThreads * U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t o = tile + u * kThreads + threadIdx.x;
+        if (o >= p.plane_vecs) break;
+        uint32_t s = o;
+        if (up) {
+          const uint32_t oy = p.div_row.div(o);
+          const uint32_t r = o - oy * p.div_row.d;
+          const uint32_t ox = p.div_vpp.div(r);
+          const uint32_t k = r - ox * p.vpp;
+          s = (oy >> 1) * in_row + (ox >> 1) * p.vpp + k;
+        }
+        v[u] = ld16(src + (size_t)s * 16);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t o = tile + u * kThreads + threadIdx.x;
+        if (o >= p.plane_vecs) break;
+        st16<NT>(dst + (size_t)o * 16, v[u]);
+      }
+    }
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// Validates an NC1HWC0-style operand: rank 5, H/W/C0 dense, N/C1 strides and
+// base 16-byte aligned.
+bool plane_dense(const thin_desc* d, int esize) {
+  if (d->rank != 5) return false;
+  const int64_t h = d->sizes[2], w = d->sizes[3], c0 = d->sizes[4];
+  if ((c0 * esize) % 16) return false;
+  if (!(c0 == 1 || d->strides[4] == 1)) return false;
+  if (!(w == 1 || d->strides[3] == c0)) return false;
+  if (!(h == 1 || d->strides[2] == w * c0)) return false;
+  return aligned16(d->data) && (d->strides[0] * esize) % 16 == 0 && (d->strides[1] * esize) % 16 == 0;
+}
+
+thin_status launch_planes(const thin_desc* ins, const int32_t* up, int count, const thin_desc* out,
+                          hipStream_t stream) {
+  const int esize = dtype_size(out->dtype);
+  PlanePlan p;
+  memset(&p, 0, sizeof p);
+  p.out = static_cast<char*>(out->data);
+  p.out_n = out->strides[0] * esize;
+  p.out_c1 = out->strides[1] * esize;
+  p.out_c1_total = (uint32_t)out->sizes[1];
+  p.oh = (uint32_t)out->sizes[2];
+  p.ow = (uint32_t)out->sizes[3];
+  p.vpp = (uint32_t)(out->sizes[4] * esize / 16);
+  p.plane_vecs = p.oh * p.ow * p.vpp;
+  p.count = count;
+  uint32_t c1 = 0;
+  for (int k = 0; k < count; ++k) {
+    p.c1_prefix[k] = c1;
+    p.src[k] = static_cast<const char*>(ins[k].data);
+    p.src_n[k] = ins[k].strides[0] * esize;
+    p.src_c1[k] = ins[k].strides[1] * esize;
+    p.up[k] = up ? (uint32_t)(up[k] != 0) : 0u;
+    c1 += (uint32_t)ins[k].sizes[1];
+  }
+  p.c1_prefix[count] = c1;
+  p.planes = (uint32_t)(out->sizes[0] * out->sizes[1]);
+  p.div_row = FastDiv::make(p.ow * p.vpp);
+  p.div_vpp = FastDiv::make(p.vpp);
+  if (p.planes == 0 || p.plane_vecs == 0) return THIN_OK;
+  const bool nt = (int64_t)p.planes * p.plane_vecs * 16 >= kStreamingStoreBytes;
+  const uint32_t gy = p.planes < 65535u ? p.planes : 65535u;
+  if (p.plane_vecs >= 2048) {
+    const uint32_t gx = (p.plane_vecs + kThreads * 2 - 1) / (kThreads * 2);
+    if (nt) hipLaunchKernelGGL((plane_kernel<2, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((plane_kernel<2, false>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+  } else {
+    const uint32_t gx = (p.plane_vecs + kThreads - 1) / kThreads;
+    if (nt) hipLaunchKernelGGL((plane_kernel<1, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((plane_kernel<1, false>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+  }
+  THIN_LAUNCH_CHECK("plane");
+  return THIN_OK;
+}
+
+// ------------------------------------------------------------ generic index map
+// Fallback for layouts the vector kernels do not take: one element per thread,
+// output element (n, c, oy, ox, k) of a 5-D view reads input (n, c, oy>>sy, ox>>sx, k).
+struct Up5Plan {
+  const char* src;
+  char* dst;
+  int64_t size[5];                 // output sizes
+  int64_t ss[5], ds[5];            // element strides
+  int32_t shift_h, shift_w;        // 1 for the upsampled axes
+  int64_t total;
+  int32_t esize;
+};
+
+template <typename E>
+__global__ __launch_bounds__(kThreads) void up5_kernel(Up5Plan p) {
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < p.total;
+       e += (int64_t)gridDim.x * kThreads) {
+    int64_t r = e, so = 0, dof = 0;
+    for (int d = 4; d >= 0; --d) {
+      const int64_t c = r % p.size[d];
+      r /= p.size[d];
+      dof += c * p.ds[d];
+      int64_t ci = c;
+      if (d == 2) ci = c >> p.shift_h;
+      if (d == 3) ci = c >> p.shift_w;
+      so += ci * p.ss[d];
+    }
+    reinterpret_cast<E*>(p.dst)[dof] = reinterpret_cast<const E*>(p.src)[so];
+  }
+}
+
+thin_status launch_up5(const thin_desc* x5, const thin_desc* y5, bool up, hipStream_t stream) {
+  Up5Plan p;
+  p.src = static_cast<const char*>(x5->data);
+  p.dst = static_cast<char*>(y5->data);
+  p.total = 1;
+  for (int d = 0; d < 5; ++d) {
+    p.size[d] = y5->sizes[d];
+    p.ss[d] = x5->strides[d];
+    p.ds[d] = y5->strides[d];
+    p.total *= p.size[d];
+  }
+  p.shift_h = up ? 1 : 0;
+  p.shift_w = up ? 1 : 0;
+  p.esize = dtype_size(y5->dtype);
+  if (p.total == 0) return THIN_OK;
+  const uint32_t grid = grid_for((uint64_t)p.total, kThreads, 1, 256u * 16u);
+  switch (p.esize) {
+    case 1: hipLaunchKernelGGL(up5_kernel<uint8_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(up5_kernel<uint16_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(up5_kernel<uint32_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+    default: hipLaunchKernelGGL(up5_kernel<uint64_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+  }
+  THIN_LAUNCH_CHECK("up5");
+  return THIN_OK;
+}
+
+// ============================================================ NCHW upsample
+// Output row vector j (8 halves) = input elements 4j..4j+3 each twice.
+struct NchwUpPlan {
+  const char* src;
+  char* dst;
+  int64_t s_n, s_c, s_h;   // input strides (bytes); w stride == element
+  int64_t d_n, d_c, d_h;   // output strides (bytes); w dense
+  uint32_t c, oh, row_vecs;  // channels, output rows, 16-byte vectors per output row
+  uint32_t rows;             // N * C * oh
+  FastDiv div_row_vecs, div_oh, div_c;
+};
+
+template <typename E, bool NT>
+__global__ __launch_bounds__(kThreads) void nchw_up_kernel(NchwUpPlan p) {
+  constexpr int PER = 16 / sizeof(E);        // output elements per vector
+  const uint32_t total = p.rows * p.row_vecs;  // < 2^31, checked on the host
+  for (uint32_t v = blockIdx.x * kThreads + threadIdx.x; v < total; v += gridDim.x * kThreads) {
+    const uint32_t row = p.div_row_vecs.div(v);
+    const uint32_t j = v - row * p.row_vecs;
+    const uint32_t nc = p.div_oh.div(row);
+    const uint32_t oy = row - nc * p.oh;
+    const uint32_t n = p.div_c.div(nc);
+    const uint32_t c = nc - n * p.c;
+    const E* s = reinterpret_cast<const E*>(p.src + n * p.s_n + c * p.s_c + (int64_t)(oy >> 1) * p.s_h) + j * (PER / 2);
+    E out[PER];
+#pragma unroll
+    for (int k = 0; k < PER / 2; ++k) {
+      E e = s[k];
+      out[2 * k] = e;
+      out[2 * k + 1] = e;
+    }
+    char* d = p.dst + n * p.d_n + c * p.d_c + (int64_t)oy * p.d_h + (size_t)j * 16;
+    st16<NT>(d, __builtin_bit_cast(u32x4, out));
+  }
+}
+
+// ============================================================ pack / unpack
+// Per (n, c1, tile of kTile pixels): LDS tile [16][kTile] of halves.
+constexpr int kTile = 256;
+
+struct PackPlan {
+  const uint16_t* x;   // NCHW fp16 bits (pack) or NC1HWC0 (unpack)
+  uint16_t* y;
+  int64_t x_n, x_c, x_hw;   // pack: NCHW strides (elements); hw = pixel stride (1 when dense)
+  int64_t y_n, y_c1;        // NC1HWC0 output strides (elements), plane dense
+  uint32_t channels;        // C
+  uint32_t c1;              // C1 = ceil(C/16)
+  uint32_t hw;              // pixels per plane
+  uint32_t tiles;           // ceil(hw / kTile)
+  uint32_t vec_ok;          // pixel rows 16-byte aligned and dense
+};
+
+// pack: NCHW -> NC1HWC0 (zero-fill channels >= C)
+__global__ __launch_bounds__(kThreads) void pack_kernel(PackPlan p) {
+  __shared__ uint16_t tile[16][kTile + 2];
+  const uint32_t t = blockIdx.x % p.tiles;
+  const uint32_t plane = blockIdx.x / p.tiles;  // n * c1 + cb
+  const uint32_t n = plane / p.c1, cb = plane - n * p.c1;
+  const uint32_t pix0 = t * kTile;
+  const uint32_t count = min((uint32_t)kTile, p.hw - pix0);
+  // load: 16 channel rows x count pixels
+  if (p.vec_ok && count == kTile) {
+    for (uint32_t k = threadIdx.x; k < 16 * (kTile / 8); k += kThreads) {
+      const uint32_t c = k / (kTile / 8), j = k % (kTile / 8);
+      const uint32_t ch = cb * 16 + c;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (ch < p.channels) v = ld16(p.x + n * p.x_n + (int64_t)ch * p.x_c + pix0 + j * 8);
+      const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) tile[c][j * 8 + q] = h[q];
+    }
+  } else {
+    for (uint32_t k = threadIdx.x; k < 16 * kTile; k += kThreads) {
+      const uint32_t c = k / kTile, j = k % kTile;
+      const uint32_t ch = cb * 16 + c;
+      uint16_t v = 0;
+      if (ch < p.channels && j < count) v = p.x[n * p.x_n + (int64_t)ch * p.x_c + (int64_t)(pix0 + j) * p.x_hw];
+      tile[c][j] = v;
+    }
+  }
+  __syncthreads();
+  // store: count pixels x 16 channels, dense in the output plane
+  uint16_t* yp = p.y + n * p.y_n + (int64_t)cb * p.y_c1 + (int64_t)pix0 * 16;
+  for (uint32_t k = threadIdx.x; k < count * 2; k += kThreads) {
+    const uint32_t pix = k >> 1, half = k & 1;
+    uint16_t h[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) h[q] = tile[half * 8 + q][pix];
+    *reinterpret_cast<u32x4*>(yp + (size_t)k * 8) = __builtin_bit_cast(u32x4, h);
+  }
+}
+
+// unpack: NC1HWC0 -> NCHW for channels < C
+__global__ __launch_bounds__(kThreads) void unpack_kernel(PackPlan p) {
+  __shared__ uint16_t tile[16][kTile + 2];
+  const uint32_t t = blockIdx.x % p.tiles;
+  const uint32_t plane = blockIdx.x / p.tiles;
+  const uint32_t n = plane / p.c1, cb = plane - n * p.c1;
+  const uint32_t pix0 = t * kTile;
+  const uint32_t count = min((uint32_t)kTile, p.hw - pix0);
+  const uint16_t* xp = p.y + n * p.y_n + (int64_t)cb * p.y_c1 + (int64_t)pix0 * 16;  // y holds the blocked source
+  for (uint32_t k = threadIdx.x; k < count * 2; k += kThreads) {
+    const uint32_t pix = k >> 1, half = k & 1;
+    u32x4 v = ld16(xp + (size_t)k * 8);
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) tile[half * 8 + q][pix] = h[q];
+  }
+  __syncthreads();
+  uint16_t* out = const_cast<uint16_t*>(p.x);  // x holds the NCHW destination
+  if (p.vec_ok && count == kTile) {
+    for (uint32_t k = threadIdx.x; k < 16 * (kTile / 8); k += kThreads) {
+      const uint32_t c = k / (kTile / 8), j = k % (kTile / 8);
+      const uint32_t ch = cb * 16 + c;
+      if (ch >= p.channels) continue;
+      uint16_t h[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) h[q] = tile[c][j * 8 + q];
+      *reinterpret_cast<u32x4*>(out + n * p.x_n + (int64_t)ch * p.x_c + pix0 + j * 8) =
+          __builtin_bit_cast(u32x4, h);
+    }
+  } else {
+    for (uint32_t k = threadIdx.x; k < 16 * kTile; k += kThreads) {
+      const uint32_t c = k / kTile, j = k % kTile;
+      const uint32_t ch = cb * 16 + c;
+      if (ch < p.channels && j < count)
+        out[n * p.x_n + (int64_t)ch * p.x_c + (int64_t)(pix0 + j) * p.x_hw] = tile[c][j];
+    }
+  }
+}
+
+// NCHW descriptor -> (n, c, hw) strides when H and W merge into one pixel axis.
+bool pixels_axis(const thin_desc* x, int64_t& hw_stride) {
+  const int64_t h = x->sizes[2], w = x->sizes[3];
+  if (h == 1) { hw_stride = w == 1 ? 1 : x->strides[3]; return true; }
+  if (w == 1) { hw_stride = x->strides[2]; return true; }
+  if (x->strides[2] != w * x->strides[3]) return false;
+  hw_stride = x->strides[3];
+  return true;
+}
+
+thin_status repack(const thin_desc* nchw, const thin_desc* blocked, bool to_blocked, hipStream_t stream) {
+  THIN_REQUIRE(desc_valid(nchw) && desc_valid(blocked), THIN_ERR_INVALID, "repack: invalid descriptor");
+  THIN_REQUIRE(nchw->rank == 4 && blocked->rank == 5 && blocked->sizes[4] == 16, THIN_ERR_INVALID,
+               "repack expects NCHW [N,C,H,W] and NC1HWC0 [N,C1,H,W,16]");
+  THIN_REQUIRE(dtype_size(nchw->dtype) == 2 && nchw->dtype == blocked->dtype, THIN_ERR_INVALID,
+               "repack supports 16-bit elements (float16) with matching dtypes");
+  const int64_t n = nchw->sizes[0], c = nchw->sizes[1], h = nchw->sizes[2], w = nchw->sizes[3];
+  const int64_t c1 = (c + 15) / 16;
+  THIN_REQUIRE(blocked->sizes[0] == n && blocked->sizes[2] == h && blocked->sizes[3] == w,
+               THIN_ERR_INVALID, "repack: N/H/W mismatch");
+  if (to_blocked)
+    THIN_REQUIRE(blocked->sizes[1] == c1, THIN_ERR_INVALID, "pack: C1 must be ceil(C/16)");
+  else
+    THIN_REQUIRE(blocked->sizes[1] * 16 >= c && blocked->sizes[1] == c1, THIN_ERR_INVALID,
+                 "unpack: C must satisfy ceil(C/16) == C1");
+  if (n * c1 * h * w == 0) return THIN_OK;
+  const bool bdense = (w == 1 || blocked->strides[3] == 16) && (h == 1 || blocked->strides[2] == w * 16) &&
+                      blocked->strides[4] == 1 && aligned16(blocked->data) && blocked->strides[0] % 8 == 0 &&
+                      blocked->strides[1] % 8 == 0;
+  int64_t hw_stride = 0;
+  const bool pix = pixels_axis(nchw, hw_stride);
+  if (!bdense || !pix) {
+    // general strides: element-wise index map through the 5-D view of NCHW
+    // (x[n, c1*16+k, h, w] <-> y[n, c1, h, w, k]); channels >= C of a pack
+    // must read as zero, which the index map cannot express, so require C%16.
+    THIN_REQUIRE(c % 16 == 0 || !to_blocked, THIN_ERR_UNSUPPORTED,
+                 "pack: non-dense layouts need C %% 16 == 0");
+    thin_desc v5 = *nchw;
+    v5.rank = 5;
+    const int64_t cs = nchw->strides[1];
+    v5.sizes[0] = n; v5.strides[0] = nchw->strides[0];
+    v5.sizes[1] = to_blocked ? c1 : blocked->sizes[1]; v5.strides[1] = cs * 16;
+    v5.sizes[2] = h; v5.strides[2] = nchw->strides[2];
+    v5.sizes[3] = w; v5.strides[3] = nchw->strides[3];
+    v5.sizes[4] = 16; v5.strides[4] = cs;
+    if (to_blocked) return launch_up5(&v5, blocked, false, stream);
+    // unpack of the first C channels only
+    thin_desc b5 = *blocked;
+    if (c % 16 == 0) return launch_up5(blocked, &v5, false, stream);
+    // partial last block: full blocks, then the tail channels
+    THIN_REQUIRE(false, THIN_ERR_UNSUPPORTED, "unpack: non-dense layout with C %% 16 != 0");
+    (void)b5;
+  }
+  PackPlan p;
+  p.x = static_cast<const uint16_t*>(nchw->data);
+  p.y = static_cast<uint16_t*>(blocked->data);
+  p.x_n = nchw->strides[0];
+  p.x_c = nchw->strides[1];
+  p.x_hw = hw_stride;
+  p.y_n = blocked->strides[0];
+  p.y_c1 = blocked->strides[1];
+  p.channels = (uint32_t)c;
+  p.c1 = (uint32_t)c1;
+  p.hw = (uint32_t)(h * w);
+  p.tiles = (p.hw + kTile - 1) / kTile;
+  p.vec_ok = (hw_stride == 1 && aligned16(nchw->data) && nchw->strides[0] % 8 == 0 && nchw->strides[1] % 8 == 0)
+                 ? 1u : 0u;
+  const uint64_t blocks = (uint64_t)n * c1 * p.tiles;
+  THIN_REQUIRE(blocks < (1ull << 31), THIN_ERR_UNSUPPORTED, "repack: too many tiles");
+  if (to_blocked)
+    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
+  THIN_LAUNCH_CHECK("repack");
+  return THIN_OK;
+}
+
+}  // namespace
+}  // namespace thin
+
+using namespace thin;
+
+extern "C" thin_status thin_cat(const thin_desc* inputs, int32_t n, int32_t dim, const thin_desc* out,
+                                hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(inputs && out && n >= 1 && n <= THIN_MAX_CAT_INPUTS, THIN_ERR_INVALID,
+               "cat: 1..%d inputs required", THIN_MAX_CAT_INPUTS);
+  THIN_REQUIRE(desc_valid(out), THIN_ERR_INVALID, "cat: invalid output descriptor");
+  THIN_REQUIRE(dim >= 0 && dim < out->rank, THIN_ERR_INVALID, "cat: dim %d out of range", dim);
+  const int esize = dtype_size(out->dtype);
+  int64_t total = 0;
+  for (int k = 0; k < n; ++k) {
+    const thin_desc* t = &inputs[k];
+    THIN_REQUIRE(desc_valid(t), THIN_ERR_INVALID, "cat: invalid input %d", k);
+    THIN_REQUIRE(t->dtype == out->dtype, THIN_ERR_INVALID, "cat requires matching dtypes");
+    THIN_REQUIRE(t->rank == out->rank, THIN_ERR_INVALID, "cat rank mismatch");
+    for (int d = 0; d < t->rank; ++d)
+      THIN_REQUIRE(d == dim || t->sizes[d] == out->sizes[d], THIN_ERR_INVALID,
+                   "cat shape mismatch outside concatenation dimension");
+    total += t->sizes[dim];
+  }
+  THIN_REQUIRE(total == out->sizes[dim], THIN_ERR_INVALID, "cat: output size along dim %d is %lld, inputs sum to %lld",
+               dim, (long long)out->sizes[dim], (long long)total);
+  if (numel(out) == 0) return THIN_OK;
+
+  // Fused launch for inputs whose rows are dense, when the output is dense.
+  const bool out_dense = is_contiguous(out);
+  int64_t inner = 1;
+  for (int d = dim + 1; d < out->rank; ++d) inner *= out->sizes[d];
+  const bool nt = numel(out) * esize >= kStreamingStoreBytes;
+  const bool out_vec = aligned16(out->data) && (out->sizes[dim] * inner * esize) % 16 == 0;
+  const thin_desc* vec_in[kCatPerLaunch];
+  int64_t vec_col[kCatPerLaunch];
+  int nv = 0;
+  const thin_desc* el_in[kCatPerLaunch];
+  int64_t el_col[kCatPerLaunch];
+  int ne = 0;
+  int64_t col = 0;
+  thin_status s = THIN_OK;
+  auto flush = [&](bool vec) -> thin_status {
+    thin_status st = THIN_OK;
+    if (vec && nv) {
+      st = launch_cat_group<u32x4>(vec_in, nv, dim, out, vec_col, esize, nt, stream);
+      nv = 0;
+    }
+    if (!vec && ne) {
+      switch (esize) {
+        case 1: st = launch_cat_group<uint8_t>(el_in, ne, dim, out, el_col, esize, false, stream); break;
+        case 2: st = launch_cat_group<uint16_t>(el_in, ne, dim, out, el_col, esize, false, stream); break;
+        case 4: st = launch_cat_group<uint32_t>(el_in, ne, dim, out, el_col, esize, false, stream); break;
+        default: st = launch_cat_group<uint64_t>(el_in, ne, dim, out, el_col, esize, false, stream); break;
+      }
+      ne = 0;
+    }
+    return st;
+  };
+  for (int k = 0; k < n; ++k) {
+    const thin_desc* t = &inputs[k];
+    const int64_t seg = t->sizes[dim];
+    if (seg == 0 || numel(t) == 0) continue;
+    if (out_dense && run_dense(t, dim)) {
+      bool vec = out_vec && aligned16(t->data) && (seg * inner * esize) % 16 == 0 && (col * inner * esize) % 16 == 0;
+      for (int d = 0; vec && d < dim; ++d) vec = (t->strides[d] * esize) % 16 == 0 || t->sizes[d] == 1;
+      if (vec) {
+        vec_in[nv] = t;
+        vec_col[nv++] = col * inner;
+        if (nv == kCatPerLaunch && (s = flush(true))) return s;
+      } else {
+        el_in[ne] = t;
+        el_col[ne++] = col * inner;
+        if (ne == kCatPerLaunch && (s = flush(false))) return s;
+      }
+    } else {
+      // strided leftover: copy into the output slice out.narrow(dim, col, seg)
+      thin_desc slice = *out;
+      slice.sizes[dim] = seg;
+      slice.data = static_cast<char*>(out->data) + col * out->strides[dim] * esize;
+      if ((s = copy_bits(t, &slice, stream))) return s;
+    }
+    col += seg;
+  }
+  if ((s = flush(true))) return s;
+  return flush(false);
+}
+
+extern "C" thin_status thin_upsample_cat_nc1hwc0(const thin_desc* inputs, const int32_t* upsample, int32_t n,
+                                                 const thin_desc* out, hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(inputs && out && n >= 1 && n <= kPlaneInputs, THIN_ERR_INVALID,
+               "upsample_cat: 1..%d inputs required", kPlaneInputs);
+  THIN_REQUIRE(desc_valid(out) && out->rank == 5, THIN_ERR_INVALID, "upsample_cat: NC1HWC0 output required");
+  const int esize = dtype_size(out->dtype);
+  int64_t c1 = 0;
+  bool fast = plane_dense(out, esize);
+  for (int k = 0; k < n; ++k) {
+    const thin_desc* t = &inputs[k];
+    const bool up = upsample && upsample[k];
+    THIN_REQUIRE(desc_valid(t) && t->rank == 5 && t->dtype == out->dtype, THIN_ERR_INVALID,
+                 "upsample_cat: input %d must be NC1HWC0 with the output dtype", k);
+    THIN_REQUIRE(t->sizes[0] == out->sizes[0] && t->sizes[4] == out->sizes[4] &&
+                 t->sizes[2] * (up ? 2 : 1) == out->sizes[2] && t->sizes[3] * (up ? 2 : 1) == out->sizes[3],
+                 THIN_ERR_INVALID, "upsample_cat: input %d has incompatible N/H/W/C0", k);
+    fast = fast && plane_dense(t, esize);
+    c1 += t->sizes[1];
+  }
+  THIN_REQUIRE(c1 == out->sizes[1], THIN_ERR_INVALID, "upsample_cat: C1 of inputs sum to %lld, output has %lld",
+               (long long)c1, (long long)out->sizes[1]);
+  if (numel(out) == 0) return THIN_OK;
+  if (fast) return launch_planes(inputs, upsample, n, out, stream);
+  // general strides: per-input element map into the output slice
+  int64_t off = 0;
+  for (int k = 0; k < n; ++k) {
+    thin_desc slice = *out;
+    slice.sizes[1] = inputs[k].sizes[1];
+    slice.data = static_cast<char*>(out->data) + off * out->strides[1] * esize;
+    thin_status s = launch_up5(&inputs[k], &slice, upsample && upsample[k], stream);
+    if (s) return s;
+    off += inputs[k].sizes[1];
+  }
+  return THIN_OK;
+}
+
+extern "C" thin_status thin_upsample2x_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_t stream) {
+  const int32_t up = 1;
+  return thin_upsample_cat_nc1hwc0(x, &up, 1, y, stream);
+}
+
+extern "C" thin_status thin_upsample2x_nchw(const thin_desc* x, const thin_desc* y, hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(desc_valid(x) && desc_valid(y) && x->rank == 4 && y->rank == 4, THIN_ERR_INVALID,
+               "upsample2x_nchw expects NCHW tensors");
+  THIN_REQUIRE(x->dtype == y->dtype, THIN_ERR_INVALID, "upsample2x_nchw requires matching dtypes");
+  THIN_REQUIRE(y->sizes[0] == x->sizes[0] && y->sizes[1] == x->sizes[1] && y->sizes[2] == 2 * x->sizes[2] &&
+               y->sizes[3] == 2 * x->sizes[3], THIN_ERR_INVALID, "upsample2x_nchw: output must be [N,C,2H,2W]");
+  if (numel(y) == 0) return THIN_OK;
+  const int esize = dtype_size(y->dtype);
+  const int64_t ow = y->sizes[3];
+  const bool vec = (esize == 2 || esize == 4) && (ow * esize) % 16 == 0 && x->strides[3] == 1 &&
+                   y->strides[3] == 1 && aligned16(y->data) && (y->strides[0] * esize) % 16 == 0 &&
+                   (y->strides[1] * esize) % 16 == 0 && (y->strides[2] * esize) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(x->data) % 8 == 0 && (x->strides[0] * esize) % 8 == 0 &&
+                   (x->strides[1] * esize) % 8 == 0 && (x->strides[2] * esize) % 8 == 0;
+  const uint64_t rows = (uint64_t)y->sizes[0] * y->sizes[1] * y->sizes[2];
+  if (!vec || rows * (uint64_t)(ow * esize / 16) >= (1ull << 31)) {
+    thin_desc x5 = *x, y5 = *y;
+    x5.rank = y5.rank = 5;
+    x5.sizes[4] = y5.sizes[4] = 1;
+    x5.strides[4] = y5.strides[4] = 1;
+    // NCHW as [N, C, H, W, 1]: the 5-D index map upsamples axes 2 and 3.
+    return launch_up5(&x5, &y5, true, stream);
+  }
+  NchwUpPlan p;
+  p.src = static_cast<const char*>(x->data);
+  p.dst = static_cast<char*>(y->data);
+  p.s_n = x->strides[0] * esize; p.s_c = x->strides[1] * esize; p.s_h = x->strides[2] * esize;
+  p.d_n = y->strides[0] * esize; p.d_c = y->strides[1] * esize; p.d_h = y->strides[2] * esize;
+  p.c = (uint32_t)y->sizes[1];
+  p.oh = (uint32_t)y->sizes[2];
+  p.row_vecs = (uint32_t)(ow * esize / 16);
+  p.rows = (uint32_t)rows;
+  p.div_row_vecs = FastDiv::make(p.row_vecs);
+  p.div_oh = FastDiv::make(p.oh);
+  p.div_c = FastDiv::make(p.c);
+  const bool nt = numel(y) * esize >= kStreamingStoreBytes;
+  const uint32_t grid = grid_for(rows * p.row_vecs, kThreads, 1, 256u * 16u);
+  if (esize == 2) {
+    if (nt) hipLaunchKernelGGL((nchw_up_kernel<uint16_t, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((nchw_up_kernel<uint16_t, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+  } else {
+    if (nt) hipLaunchKernelGGL((nchw_up_kernel<uint32_t, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((nchw_up_kernel<uint32_t, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+  }
+  THIN_LAUNCH_CHECK("nchw_up");
+  return THIN_OK;
+}
+
+extern "C" thin_status thin_pack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_t stream) {
+  clear_error();
+  return repack(x, y, true, stream);
+}
+
+extern "C" thin_status thin_unpack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_t stream) {
+  clear_error();
+  return repack(y, x, false, stream);
+}
