@@ -136,17 +136,115 @@ def op_silu_add(capi, dev, n, rotate=True):
     return launch, sets, per * 3
 
 
+def rotated(make, per_set_bytes, rotate):
+    n = rotation_count(per_set_bytes) if rotate else 1
+    return [make(i) for i in range(n)]
+
+
+def op_pack(capi, dev, n, rotate=True):
+    """C1 repack NCHW [n,64,160,160] -> NC1HWC0 [n,4,160,160,16]."""
+    per = n * 64 * 160 * 160 * 2
+    g = torch.Generator(device=dev).manual_seed(5)
+    sets = rotated(lambda i: (torch.randn((n, 64, 160, 160), generator=g, device=dev).half(),
+                              torch.empty((n, 4, 160, 160, 16), dtype=torch.float16, device=dev)), per * 2, rotate)
+    return (lambda st: capi.pack_nc1hwc0(st[0], out=st[1])), sets, per * 2
+
+
+def op_cat_c2f(capi, dev, n, rotate=True):
+    """C3 C2f cat of 4 chunks [n,64,80,80] (two halves of one [n,128,80,80])."""
+    chunk = n * 4 * 80 * 80 * 16 * 2
+
+    def make(i):
+        parent = blocked_normal(n, 128, 80, 80, 30 + i, dev)
+        return (parent, blocked_normal(n, 64, 80, 80, 60 + i, dev), blocked_normal(n, 64, 80, 80, 90 + i, dev),
+                torch.empty((n, 16, 80, 80, 16), dtype=torch.float16, device=dev))
+    sets = rotated(make, chunk * 8, rotate)
+
+    def launch(st):
+        a, b = st[0][:, :4], st[0][:, 4:]
+        capi.cat([a, b, st[1], st[2]], 1, out=st[3])
+    return launch, sets, chunk * 8
+
+
+def op_upsample(capi, dev, n, rotate=True):
+    """C3 nearest 2x [n,256,40,40] -> [n,256,80,80] in NC1HWC0."""
+    src = n * 16 * 40 * 40 * 16 * 2
+    sets = rotated(lambda i: (blocked_normal(n, 256, 40, 40, 120 + i, dev),
+                              torch.empty((n, 16, 80, 80, 16), dtype=torch.float16, device=dev)), src * 5, rotate)
+    return (lambda st: capi.upsample2x_nc1hwc0(st[0], out=st[1])), sets, src * 5
+
+
+def op_upsample_cat(capi, dev, n, rotate=True):
+    """C3 fused: cat(up2x([n,256,40,40]), [n,128,80,80]) -> [n,384,80,80]."""
+    up = n * 16 * 40 * 40 * 16 * 2
+    other = n * 8 * 80 * 80 * 16 * 2
+    algo = up + other + n * 24 * 80 * 80 * 16 * 2
+    sets = rotated(lambda i: (blocked_normal(n, 256, 40, 40, 150 + i, dev), blocked_normal(n, 128, 80, 80, 180 + i, dev),
+                              torch.empty((n, 24, 80, 80, 16), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.upsample_cat_nc1hwc0([st[0], st[1]], [True, False], out=st[2])), sets, algo
+
+
+def op_dfl(capi, dev, n, rotate=True):
+    """C4 DFL [n,64,8400] -> [n,4,8400] fp16."""
+    algo = n * (64 * 8400 * 2 + 4 * 8400 * 2)
+    g = torch.Generator(device=dev).manual_seed(4)
+    sets = rotated(lambda i: ((torch.randn((n, 64, 8400), generator=g, device=dev) * 3).half(),
+                              torch.empty((n, 4, 8400), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.dfl_expect(st[0], out=st[1])), sets, algo
+
+
+def op_sigmoid(capi, dev, n, rotate=True):
+    """C4 class sigmoid [n,80,8400]."""
+    algo = n * 80 * 8400 * 2 * 2
+    g = torch.Generator(device=dev).manual_seed(14)
+    sets = rotated(lambda i: ((torch.randn((n, 80, 8400), generator=g, device=dev) * 2 - 4).half(),
+                              torch.empty((n, 80, 8400), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.unary(capi.SIGMOID, st[0], out=st[1])), sets, algo
+
+
+def op_softmax(capi, dev, n, rotate=True):
+    """C5 attention row softmax [n,4,400,400]."""
+    algo = n * 4 * 400 * 400 * 2 * 2
+    g = torch.Generator(device=dev).manual_seed(5)
+    sets = rotated(lambda i: ((torch.randn((n, 4, 400, 400), generator=g, device=dev) * 2).half(),
+                              torch.empty((n, 4, 400, 400), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.softmax(st[0], 3, out=st[1])), sets, algo
+
+
+def op_select(capi, dev, layout, rotate=False):
+    """C5 NMS-free top-300 of [1,8400,84] (latency-bound: report us)."""
+    from tests.selection_fixtures import c5_selection_input  # input generator, shared with the tests
+    x = c5_selection_input()
+    base = x.transpose(1, 2).contiguous() if layout == "transposed" else x.contiguous()
+    d = base.to(dev)
+    view = d.transpose(1, 2) if layout == "transposed" else d
+    out = torch.empty((1, 300, 6), dtype=torch.float32, device=dev)
+    ws = torch.empty(capi.detection_select_workspace(1, 8400, 80, 300, False), dtype=torch.uint8, device=dev)
+    algo = 8400 * 84 * 2 + 300 * 6 * 4
+    return (lambda st: capi.detection_select(view, 300, False, out=out, workspace=ws)), [None], algo
+
+
 def op_rows(capi, dev):
     """(name, cfg, N, factory) for the per-op table."""
     rows = []
     for n in (1, 32):
         rows.append(("silu_add", "C1", n, lambda r, n=n: op_silu_add(capi, dev, n, r)))
+        rows.append(("pack_nc1hwc0", "C1", n, lambda r, n=n: op_pack(capi, dev, n, r)))
     for n in (1, 32):
         for (c, h, w) in C2_SHAPES:
             for narrowed in (False, True):
                 name = f"affine_silu{'_narrowed' if narrowed else ''}_{c}x{h}x{w}"
                 rows.append((name, "C2", n, lambda r, n=n, c=c, h=h, w=w, nr=narrowed:
                              op_affine_silu(capi, dev, n, c, h, w, nr, r)))
+    for n in (1, 32):
+        rows.append(("cat_c2f_4x64", "C3", n, lambda r, n=n: op_cat_c2f(capi, dev, n, r)))
+        rows.append(("upsample2x_256x40x40", "C3", n, lambda r, n=n: op_upsample(capi, dev, n, r)))
+        rows.append(("upsample_cat_256+128", "C3", n, lambda r, n=n: op_upsample_cat(capi, dev, n, r)))
+        rows.append(("dfl_expect_64x8400", "C4", n, lambda r, n=n: op_dfl(capi, dev, n, r)))
+        rows.append(("sigmoid_80x8400", "C4", n, lambda r, n=n: op_sigmoid(capi, dev, n, r)))
+        rows.append(("softmax_4x400x400", "C5", n, lambda r, n=n: op_softmax(capi, dev, n, r)))
+    for layout in ("contiguous", "transposed"):
+        rows.append((f"detection_select_{layout}", "C5", 1, lambda r, l=layout: op_select(capi, dev, l)))
     return rows
 
 
@@ -200,8 +298,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
     ap.add_argument("--iters", type=int, default=200, help="launches per per-op timing round")
-    ap.add_argument("--profile", action="store_true",
-                    help="only replay the dominant kernel (for rocprofv3 summaries); prints its timing")
+    ap.add_argument("--profile", choices=["dominant", "copy"], default=None,
+                    help="only replay the dominant kernel, or a plain 16-byte copy of the same size "
+                         "(rocprofv3 summaries / counter calibration); prints its timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of "
@@ -216,8 +315,14 @@ def main():
     n = 32
     if args.profile:
         launch, sets, algo = op_affine_silu(capi, dev, n, *C2_SHAPES[0], False, rotate=True)
+        what = "affine_silu N=32 C,H,W=(128,80,80)"
+        if args.profile == "copy":
+            sets = [(st[0], st[3]) for st in sets]
+            launch = lambda st: capi.copy(st[0], st[1])  # noqa: E731
+            what = "copy of the same [32,8,80,80,16] fp16 tensor (104857600 B read + written)"
+            algo = 2 * sets[0][0].numel() * 2
         t = time_launches(launch, sets, args.iters)
-        print(json.dumps({"profile": "affine_silu N=32 C,H,W=(128,80,80)", "us": round(t * 1e6, 3),
+        print(json.dumps({"profile": what, "us": round(t * 1e6, 3),
                           "GB/s": round(algo / t / 1e9, 1), "launches": args.iters * 6 + 3}))
         return
 
@@ -274,7 +379,8 @@ def main():
     ops = []
     if not args.no_ops:
         for name, cfg, nn, factory in op_rows(capi, dev):
-            for rotate in ((False, True) if nn == 1 else (True,)):
+            modes = (False,) if name.startswith("detection_select") else ((False, True) if nn == 1 else (True,))
+            for rotate in modes:
                 launch, sets, algo = factory(rotate)
                 t = time_launches(launch, sets, args.iters)
                 gbs = algo / t / 1e9

@@ -262,14 +262,14 @@ def detection_select_workspace(b: int, a: int, nc: int, max_det: int, agnostic: 
 
 
 def detection_select(decoded, max_det: int, agnostic: bool = False, trace: bool = False,
-                     stream=None):
+                     stream=None, out=None, workspace=None):
     b, a, ch = decoded.shape
     nc = ch - 4
     k = min(max_det, a)
     dev = decoded.device
-    out = torch.empty((b, k, 6), dtype=torch.float32, device=dev)
+    out = torch.empty((b, k, 6), dtype=torch.float32, device=dev) if out is None else out
     ws_bytes = detection_select_workspace(b, a, nc, max_det, agnostic)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if workspace is None else workspace
     tr = None
     tensors = None
     if trace:

@@ -17,6 +17,8 @@
 
 #include <string.h>
 
+#include <type_traits>
+
 namespace thin {
 namespace {
 
@@ -170,7 +172,20 @@ __device__ __forceinline__ void store16(void* dst, const W& w) {
   else *reinterpret_cast<u32x4*>(dst) = bits;
 }
 
-// Output size from which the streaming store is used.
+template <bool NT, typename W>
+__device__ __forceinline__ W load16(const void* src) {
+  static_assert(sizeof(W) == 16, "16-byte load");
+  u32x4 bits = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src))
+                  : *reinterpret_cast<const u32x4*>(src);
+  return __builtin_bit_cast(W, bits);
+}
+
+// Outputs of at least this many bytes are written with streaming
+// (non-temporal) stores; smaller ones keep cached stores so that the next
+// kernel finds them in L2 / MALL.  Measured on gfx950 with the Infinity Cache
+// defeated: 256-thread blocks with two 16-byte vectors per thread, cached
+// loads and streaming stores beat 1024-thread blocks with eight vectors and
+// non-temporal loads for every kernel here except a bare copy.
 constexpr int64_t kStreamingStoreBytes = (int64_t)16 << 20;
 
 // Unit offsets for the vector kernel; ND == 1 means every operand is flat
@@ -203,15 +218,17 @@ __device__ __forceinline__ void unit_offsets(const MapPlan<NIN>& p, uint32_t e, 
 // units tile + u*kThreads + t, so every load/store instruction of a wave
 // covers 64 consecutive 16-byte vectors when the operand is dense.  All U
 // loads are issued before any math to keep several vectors in flight.
-template <typename T, int V, int NIN, int ND, int U, bool NT, class Op>
-__global__ __launch_bounds__(kThreads) void map_vec_kernel(MapPlan<NIN> p) {
-  const uint32_t tile_units = kThreads * U;
+template <typename T, int V, int NIN, int ND, int U, bool NT, class Op, uint32_t BS>
+__global__ __launch_bounds__(BS) void map_vec_kernel(MapPlan<NIN> p) {
+  const uint32_t tile_units = BS * U;
   for (uint32_t tile = blockIdx.x * tile_units; tile < p.units; tile += gridDim.x * tile_units) {
-    T val[U][V][NIN];
+    // raw 16-byte vectors only: unpacking is deferred to the compute phase so
+    // that U * NIN vectors in flight cost 4 VGPRs each
+    VecT<T, V> raw[U][NIN];
     int32_t oo[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t unit = tile + u * kThreads + threadIdx.x;
+      const uint32_t unit = tile + u * BS + threadIdx.x;
       if (unit >= p.units) break;
       int32_t io[NIN];
       unit_offsets<NIN, ND>(p, unit * (uint32_t)V, oo[u], io);
@@ -219,31 +236,41 @@ __global__ __launch_bounds__(kThreads) void map_vec_kernel(MapPlan<NIN> p) {
       for (int k = 0; k < NIN; ++k) {
         const T* src = static_cast<const T*>(p.in[k]) + io[k];
         if (p.in_mode[k] == kVec) {
-          VecT<T, V> w = *reinterpret_cast<const VecT<T, V>*>(src);
-#pragma unroll
-          for (int j = 0; j < V; ++j) val[u][j][k] = w.v[j];
+          raw[u][k] = load16<false, VecT<T, V>>(src);
         } else if (p.in_mode[k] == kBcast) {
-          T sv = *src;
+          const T sv = *src;
 #pragma unroll
-          for (int j = 0; j < V; ++j) val[u][j][k] = sv;
+          for (int j = 0; j < V; ++j) raw[u][k].v[j] = sv;
         } else {
           const int32_t st = p.istride[k][0];
 #pragma unroll
-          for (int j = 0; j < V; ++j) val[u][j][k] = src[j * st];
+          for (int j = 0; j < V; ++j) raw[u][k].v[j] = src[j * st];
         }
       }
     }
     const Op op;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t unit = tile + u * kThreads + threadIdx.x;
+      const uint32_t unit = tile + u * BS + threadIdx.x;
       if (unit >= p.units) break;
+      if constexpr (std::is_same<Op, OpCopy>::value) {
+        // bit copy: move the 16-byte word as is
+        T* dst = static_cast<T*>(p.out) + oo[u];
+        if (p.out_mode == kVec) {
+          store16<NT>(dst, raw[u][0]);
+        } else {
+          const int32_t st = p.ostride[0];
+#pragma unroll
+          for (int j = 0; j < V; ++j) dst[j * st] = raw[u][0].v[j];
+        }
+        continue;
+      }
       VecT<T, V> r;
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         T lane[NIN];
 #pragma unroll
-        for (int k = 0; k < NIN; ++k) lane[k] = val[u][j][k];
+        for (int k = 0; k < NIN; ++k) lane[k] = raw[u][k].v[j];
         r.v[j] = op.template operator()<T, NIN>(lane, p.pa, p.pb);
       }
       T* dst = static_cast<T*>(p.out) + oo[u];
@@ -343,9 +370,7 @@ bool try_affine_blocked(const thin_desc* x, const thin_desc* sc, const thin_desc
   if (!dense_plane(x) || !dense_plane(out) || !per_channel(sc) || !per_channel(b)) return false;
   const int64_t planes = x->sizes[0] * x->sizes[1];
   const int64_t plane_vecs = h * w * 2;
-  const int64_t span = (x->sizes[0] - 1) * x->strides[0] + (x->sizes[1] - 1) * x->strides[1] + plane_vecs * 8;
-  if (planes >= ((int64_t)1 << 31) || plane_vecs >= ((int64_t)1 << 30) || span >= ((int64_t)1 << 40))
-    return false;
+  if (planes >= ((int64_t)1 << 31) || plane_vecs >= ((int64_t)1 << 30)) return false;
   AffinePlan p;
   p.x = static_cast<const _Float16*>(x->data);
   p.s = static_cast<const _Float16*>(sc->data);
@@ -383,13 +408,15 @@ template <typename T, int NIN, int ND, class Op>
 void launch_plan(const MapPlan<NIN>& p, bool vec, bool nt, hipStream_t stream) {
   constexpr int V = 16 / (int)sizeof(T);
   if (vec) {
-    uint32_t grid = grid_for(p.units, kThreads, kUnroll, 256u * 64u);
-    if (nt)
-      hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, kUnroll, true, Op>), dim3(grid), dim3(kThreads),
-                         0, stream, p);
-    else
-      hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, kUnroll, false, Op>), dim3(grid), dim3(kThreads),
-                         0, stream, p);
+    if (nt) {
+      uint32_t grid = grid_for(p.units, kThreads, kUnroll, 256u * 64u);
+      hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, kUnroll, true, Op, kThreads>), dim3(grid),
+                         dim3(kThreads), 0, stream, p);
+    } else {
+      uint32_t grid = grid_for(p.units, kThreads, kUnroll, 256u * 64u);
+      hipLaunchKernelGGL((map_vec_kernel<T, V, NIN, ND, kUnroll, false, Op, kThreads>), dim3(grid),
+                         dim3(kThreads), 0, stream, p);
+    }
   } else {
     uint32_t grid = grid_for(p.units, kThreads, 1, 256u * 16u);
     hipLaunchKernelGGL((map_scalar_kernel<T, NIN, ND, Op>), dim3(grid), dim3(kThreads), 0, stream, p);

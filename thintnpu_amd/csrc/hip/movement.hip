@@ -28,6 +28,10 @@ __device__ __forceinline__ void st16(void* dst, u32x4 v) {
 }
 __device__ __forceinline__ u32x4 ld16(const void* src) { return *reinterpret_cast<const u32x4*>(src); }
 
+// Large outputs (>= kStreamingStoreBytes) are written with streaming stores;
+// loads stay cached (see the launch-shape note in elementwise.hip).
+constexpr uint32_t kStreamThreads = 256;
+
 // ============================================================ cat
 
 constexpr int kCatPerLaunch = 16;
@@ -50,36 +54,58 @@ struct CatPlan {
 // Units of type W (16-byte vectors or single elements).  A block copies one
 // chunk (kThreads * U units) of one (input, row) run; all index math except
 // the unit offset is uniform per block.
-template <typename W, int U, bool NT>
-__global__ __launch_bounds__(kThreads) void cat_kernel(CatPlan p) {
+template <typename W, int U, bool NT, uint32_t BS>
+__global__ __launch_bounds__(BS) void cat_kernel(CatPlan p) {
   const uint32_t task = blockIdx.x;
-  int i = 0;
-  while (i + 1 < p.count && task >= p.chunks_prefix[i + 1]) ++i;
-  const uint32_t local = task - p.chunks_prefix[i];
-  const uint32_t row = local / p.chunks_per_row[i];
-  const uint32_t chunk = local - row * p.chunks_per_row[i];
+  // Select this block's input with compile-time indices only: indexing the
+  // by-value plan with a runtime index would force it into scratch memory.
+  const char* src_base = p.src[0];
+  int64_t col = p.col_offset[0], n = p.run_units[0];
+  uint32_t first = 0, cpr = p.chunks_per_row[0];
+  int64_t ostr[kCatOuterDims];
+#pragma unroll
+  for (int d = 0; d < kCatOuterDims; ++d) ostr[d] = p.src_outer_stride[0][d];
+#pragma unroll
+  for (int j = 1; j < kCatPerLaunch; ++j) {
+    if (j < p.count && task >= p.chunks_prefix[j]) {
+      src_base = p.src[j];
+      col = p.col_offset[j];
+      n = p.run_units[j];
+      first = p.chunks_prefix[j];
+      cpr = p.chunks_per_row[j];
+#pragma unroll
+      for (int d = 0; d < kCatOuterDims; ++d) ostr[d] = p.src_outer_stride[j][d];
+    }
+  }
+  const uint32_t local = task - first;
+  const uint32_t row = local / cpr;
+  const uint32_t chunk = local - row * cpr;
   // row offset of the source: decompose row over the shared outer sizes
   int64_t src_off = 0;
   uint64_t r = row;
-  for (int d = p.n_outer - 1; d >= 0; --d) {
+#pragma unroll
+  for (int d = kCatOuterDims - 1; d >= 0; --d) {
+    if (d >= p.n_outer) continue;
     const uint64_t sz = (uint64_t)p.outer_size[d];
     const uint64_t c = r % sz;
     r /= sz;
-    src_off += (int64_t)c * p.src_outer_stride[i][d];
+    src_off += (int64_t)c * ostr[d];
   }
-  const W* src = reinterpret_cast<const W*>(p.src[i] + src_off);
-  W* dst = reinterpret_cast<W*>(p.out + (int64_t)row * p.out_row + p.col_offset[i]);
-  const int64_t base = (int64_t)chunk * kThreads * U;
-  const int64_t n = p.run_units[i];
+  const W* src = reinterpret_cast<const W*>(src_base + src_off);
+  W* dst = reinterpret_cast<W*>(p.out + (int64_t)row * p.out_row + col);
+  const int64_t base = (int64_t)chunk * BS * U;
   W v[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t k = base + u * kThreads + threadIdx.x;
-    if (k < n) v[u] = src[k];
+    const int64_t k = base + u * BS + threadIdx.x;
+    if (k < n) {
+      if constexpr (sizeof(W) == 16) v[u] = __builtin_bit_cast(W, ld16(src + k));
+      else v[u] = src[k];
+    }
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t k = base + u * kThreads + threadIdx.x;
+    const int64_t k = base + u * BS + threadIdx.x;
     if (k < n) {
       if constexpr (sizeof(W) == 16) st16<NT>(dst + k, __builtin_bit_cast(u32x4, v[u]));
       else dst[k] = v[u];
@@ -102,7 +128,9 @@ bool run_dense(const thin_desc* t, int dim) {
 template <typename W>
 thin_status launch_cat_group(const thin_desc* const* ins, int count, int dim, const thin_desc* out,
                              const int64_t* col_elems, int esize, bool nt, hipStream_t stream) {
-  constexpr int U = 4;
+  const bool stream_cfg = nt && sizeof(W) == 16;
+  const int U = 4;
+  const int64_t BS = stream_cfg ? kStreamThreads : kThreads;
   const int64_t wsize = sizeof(W);
   CatPlan p;
   memset(&p, 0, sizeof p);
@@ -123,7 +151,7 @@ thin_status launch_cat_group(const thin_desc* const* ins, int count, int dim, co
     p.col_offset[k] = col_elems[k] * esize;
     const int64_t run_bytes = t->sizes[dim] * inner * esize;
     p.run_units[k] = run_bytes / wsize;
-    const int64_t cpr = (p.run_units[k] + kThreads * U - 1) / (kThreads * U);
+    const int64_t cpr = (p.run_units[k] + BS * U - 1) / (BS * U);
     p.chunks_per_row[k] = (uint32_t)cpr;
     p.chunks_prefix[k] = (uint32_t)total;
     total += (uint64_t)cpr * (uint64_t)outer;
@@ -132,10 +160,11 @@ thin_status launch_cat_group(const thin_desc* const* ins, int count, int dim, co
   THIN_REQUIRE(total < (1ull << 31), THIN_ERR_UNSUPPORTED, "cat: too many row chunks (%llu)",
                (unsigned long long)total);
   if (total == 0) return THIN_OK;
-  if (nt && wsize == 16)
-    hipLaunchKernelGGL((cat_kernel<W, U, true>), dim3((uint32_t)total), dim3(kThreads), 0, stream, p);
+  if (stream_cfg)
+    hipLaunchKernelGGL((cat_kernel<W, 4, true, kStreamThreads>), dim3((uint32_t)total), dim3(kStreamThreads), 0,
+                       stream, p);
   else
-    hipLaunchKernelGGL((cat_kernel<W, U, false>), dim3((uint32_t)total), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((cat_kernel<W, 4, false, kThreads>), dim3((uint32_t)total), dim3(kThreads), 0, stream, p);
   THIN_LAUNCH_CHECK("cat");
   return THIN_OK;
 }
@@ -159,44 +188,49 @@ struct PlanePlan {
   int64_t src_n[kPlaneInputs], src_c1[kPlaneInputs];  // bytes
   uint32_t up[kPlaneInputs];   // 1 = upsample 2x
   uint32_t planes;             // N * out_c1_total
+  uint32_t units;              // planes * plane_vecs
   FastDiv div_row;             // ow * vpp (vectors per output row)
   FastDiv div_vpp;
+  FastDiv div_plane;           // plane_vecs
+  FastDiv div_c1;              // out_c1_total
 };
 
-template <int U, bool NT>
-__global__ __launch_bounds__(kThreads) void plane_kernel(PlanePlan p) {
-  for (uint32_t plane = blockIdx.y; plane < p.planes; plane += gridDim.y) {
-    const uint32_t n = plane / p.out_c1_total;
-    const uint32_t c1 = plane - n * p.out_c1_total;
-    int i = 0;
-    while (i + 1 < p.count && c1 >= p.c1_prefix[i + 1]) ++i;
-    const uint32_t ic1 = c1 - p.c1_prefix[i];
-    const char* src = p.src[i] + (int64_t)n * p.src_n[i] + (int64_t)ic1 * p.src_c1[i];
-    char* dst = p.out + (int64_t)n * p.out_n + (int64_t)c1 * p.out_c1;
-    const bool up = p.up[i] != 0;
-    const uint32_t in_row = (p.ow >> 1) * p.vpp;  // vectors per input row (upsample)
-    for (uint32_t tile = blockIdx.x * kThreads * U; tile < p.plane_vecs; tile += gridDim.x * kThreads * U) {
-      u32x4 v[U];
+// Flat over all output vectors v of the (virtually dense) [N, C1, plane] space.
+template <int U, bool NT, uint32_t BS>
+__global__ __launch_bounds__(BS) void plane_kernel(PlanePlan p) {
+  const uint32_t in_row = (p.ow >> 1) * p.vpp;  // vectors per input row (upsample)
+  for (uint32_t tile = blockIdx.x * BS * U; tile < p.units; tile += gridDim.x * BS * U) {
+    u32x4 v[U];
+    char* dst[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const uint32_t o = tile + u * kThreads + threadIdx.x;
-        if (o >= p.plane_vecs) break;
-        uint32_t s = o;
-        if (up) {
-          const uint32_t oy = p.div_row.div(o);
-          const uint32_t r = o - oy * p.div_row.d;
-          const uint32_t ox = p.div_vpp.div(r);
-          const uint32_t k = r - ox * p.vpp;
-          s = (oy >> 1) * in_row + (ox >> 1) * p.vpp + k;
-        }
-        v[u] = ld16(src + (size_t)s * 16);
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = tile + u * BS + threadIdx.x;
+      if (g >= p.units) break;
+      const uint32_t plane = p.div_plane.div(g);
+      const uint32_t o = g - plane * p.plane_vecs;
+      const uint32_t n = p.div_c1.div(plane);
+      const uint32_t c1 = plane - n * p.out_c1_total;
+      int i = 0;
+      while (i + 1 < p.count && c1 >= p.c1_prefix[i + 1]) ++i;
+      const uint32_t ic1 = c1 - p.c1_prefix[i];
+      const char* src = p.src[i] + (int64_t)n * p.src_n[i] + (int64_t)ic1 * p.src_c1[i];
+      dst[u] = p.out + (int64_t)n * p.out_n + (int64_t)c1 * p.out_c1 + (size_t)o * 16;
+      if (p.up[i]) {
+        const uint32_t oy = p.div_row.div(o);
+        const uint32_t r = o - oy * p.div_row.d;
+        const uint32_t ox = p.div_vpp.div(r);
+        const uint32_t k = r - ox * p.vpp;
+        // each source vector feeds four outputs: keep it cacheable
+        v[u] = ld16(src + (size_t)((oy >> 1) * in_row + (ox >> 1) * p.vpp + k) * 16);
+      } else {
+        v[u] = ld16(src + (size_t)o * 16);
       }
+    }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const uint32_t o = tile + u * kThreads + threadIdx.x;
-        if (o >= p.plane_vecs) break;
-        st16<NT>(dst + (size_t)o * 16, v[u]);
-      }
+    for (int u = 0; u < U; ++u) {
+      const uint32_t g = tile + u * BS + threadIdx.x;
+      if (g >= p.units) break;
+      st16<NT>(dst[u], v[u]);
     }
   }
 }
@@ -243,16 +277,17 @@ thin_status launch_planes(const thin_desc* ins, const int32_t* up, int count, co
   p.div_row = FastDiv::make(p.ow * p.vpp);
   p.div_vpp = FastDiv::make(p.vpp);
   if (p.planes == 0 || p.plane_vecs == 0) return THIN_OK;
-  const bool nt = (int64_t)p.planes * p.plane_vecs * 16 >= kStreamingStoreBytes;
-  const uint32_t gy = p.planes < 65535u ? p.planes : 65535u;
-  if (p.plane_vecs >= 2048) {
-    const uint32_t gx = (p.plane_vecs + kThreads * 2 - 1) / (kThreads * 2);
-    if (nt) hipLaunchKernelGGL((plane_kernel<2, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL((plane_kernel<2, false>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+  const uint64_t units = (uint64_t)p.planes * p.plane_vecs;
+  THIN_REQUIRE(units < (1ull << 31), THIN_ERR_UNSUPPORTED, "upsample/cat: output too large for one launch");
+  p.units = (uint32_t)units;
+  p.div_plane = FastDiv::make(p.plane_vecs);
+  p.div_c1 = FastDiv::make(p.out_c1_total);
+  if ((int64_t)units * 16 >= kStreamingStoreBytes) {
+    const uint32_t grid = grid_for(units, kStreamThreads, 2, 256u * 64u);
+    hipLaunchKernelGGL((plane_kernel<2, true, kStreamThreads>), dim3(grid), dim3(kStreamThreads), 0, stream, p);
   } else {
-    const uint32_t gx = (p.plane_vecs + kThreads - 1) / kThreads;
-    if (nt) hipLaunchKernelGGL((plane_kernel<1, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL((plane_kernel<1, false>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
+    const uint32_t grid = grid_for(units, kThreads, 2, 256u * 64u);
+    hipLaunchKernelGGL((plane_kernel<2, false, kThreads>), dim3(grid), dim3(kThreads), 0, stream, p);
   }
   THIN_LAUNCH_CHECK("plane");
   return THIN_OK;
@@ -368,6 +403,7 @@ struct PackPlan {
 };
 
 // pack: NCHW -> NC1HWC0 (zero-fill channels >= C)
+template <bool NT>
 __global__ __launch_bounds__(kThreads) void pack_kernel(PackPlan p) {
   __shared__ uint16_t tile[16][kTile + 2];
   const uint32_t t = blockIdx.x % p.tiles;
@@ -403,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackPlan p) {
     uint16_t h[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) h[q] = tile[half * 8 + q][pix];
-    *reinterpret_cast<u32x4*>(yp + (size_t)k * 8) = __builtin_bit_cast(u32x4, h);
+    st16<NT>(yp + (size_t)k * 8, __builtin_bit_cast(u32x4, h));
   }
 }
 
@@ -515,8 +551,11 @@ thin_status repack(const thin_desc* nchw, const thin_desc* blocked, bool to_bloc
                  ? 1u : 0u;
   const uint64_t blocks = (uint64_t)n * c1 * p.tiles;
   THIN_REQUIRE(blocks < (1ull << 31), THIN_ERR_UNSUPPORTED, "repack: too many tiles");
-  if (to_blocked)
-    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
+  const bool nt = n * c1 * h * w * 32 >= kStreamingStoreBytes;
+  if (to_blocked && nt)
+    hipLaunchKernelGGL(pack_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
+  else if (to_blocked)
+    hipLaunchKernelGGL(pack_kernel<false>, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
   else
     hipLaunchKernelGGL(unpack_kernel, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
   THIN_LAUNCH_CHECK("repack");
