@@ -1,0 +1,334 @@
+"""The PrivateUse1 ("npu") drop-in surface on the GPU: aten registrations,
+thin_backend / thin_native_flow / thin_blocked / thin_fused ops, and the
+CapturedForward / FrozenGraph capture-replay contract -- restating the
+reference's verify_ops.py, verify_graph.py, verify_aten.py, verify_all.py,
+verify_cat_plan.py, verify_dfl_softmax.py and verify_selection_flow.py device
+checks.  Values are compared with the same CPU oracle as the C-ABI tests."""
+import math
+import threading
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import elementwise as ew
+from oracle import movement as mv
+from oracle import reductions as rd
+from oracle import selection as sel
+from oracle.numerics import assert_rel, assert_ulp, bits_equal
+from tests.helpers import gen, normal16, random_bits16, to_blocked
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def npu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device visible")
+    import thin_backend
+    thin_backend.load_flow_libraries()
+    return torch.device("npu:0")
+
+
+def close(a, b, tol):
+    assert a.device.type == "npu"
+    got = a.cpu()
+    assert got.shape == b.shape and got.dtype == b.dtype
+    if got.dtype == torch.float16:
+        assert_ulp(got, b, tol)
+    else:
+        torch.testing.assert_close(got, b, rtol=1e-5, atol=1e-5, equal_nan=True)
+
+
+def test_binary_views_and_cat(npu):
+    """verify_ops.py:68-143 restated."""
+    g = gen(42)
+    with torch.inference_mode():
+        for dtype in (torch.float32, torch.float16):
+            for shape in ((1,), (7,), (2047,), (2049,), (65537,), (0,), (), (3, 5, 7)):
+                a = (torch.rand(shape, generator=g) * 2 - 1).to(dtype)
+                b = (torch.rand(shape, generator=g) + 0.5).to(dtype)
+                x, y = a.to(npu), b.to(npu)
+                for op in ("sub", "mul", "div", "add"):
+                    close(getattr(torch, op)(x, y), getattr(torch, op)(a, b), 0)
+            a = torch.rand(2, 5, 7, generator=g).to(dtype)
+            b = (torch.rand(2, 5, 7, generator=g) + 0.5).to(dtype)
+            close(torch.sub(a.to(npu).transpose(0, 2), b.to(npu).transpose(0, 2)),
+                  torch.sub(a.transpose(0, 2), b.transpose(0, 2)), 0)
+            close(torch.sub(a.to(npu), b.to(npu), alpha=2), torch.sub(a, b, alpha=2), 0)
+            close(a.to(npu) * 0.5, a * 0.5, 0)
+            close(a.to(npu) + 1.25, a + 1.25, 0)
+            # cat / split aliasing
+            for dim in (0, 1, 2, -1):
+                shape_b = [3, 5, 7]
+                shape_b[dim % 3] = 4
+                p, q = torch.randn(3, 5, 7, generator=g).to(dtype), torch.randn(shape_b, generator=g).to(dtype)
+                assert bits_equal(torch.cat((p.to(npu), q.to(npu), p.to(npu)), dim).cpu(), torch.cat((p, q, p), dim))
+            x = a.to(npu)
+            for dim in (0, 1, 2):
+                parts = torch.split(x, 2, dim)
+                for part, ref in zip(parts, torch.split(a, 2, dim)):
+                    assert part.untyped_storage().data_ptr() == x.untyped_storage().data_ptr()
+                    assert bits_equal(part.cpu(), ref)
+                assert bits_equal(torch.cat(parts, dim).cpu(), a)
+            empty = torch.empty(0, dtype=dtype).to(npu)
+            assert bits_equal(torch.cat((empty, x, empty), 1).cpu(), a)
+            # views keep metadata
+            for view in (lambda t: t.view(10, 7), lambda t: t.transpose(0, 2), lambda t: t.unsqueeze(1),
+                         lambda t: t.unsqueeze(0).expand(4, -1, -1, -1), lambda t: t.as_strided((2, 3), (21, 7), 1)):
+                v, r = view(x), view(a)
+                assert v.stride() == r.stride() and v.storage_offset() == r.storage_offset()
+                assert bits_equal(v.cpu(), r)
+
+
+def test_silu_chain_in_place(npu):
+    """silu_ on strided parents and the C2f split -> silu_ -> add -> cat chain."""
+    with torch.inference_mode():
+        for dtype in (torch.float32, torch.float16):
+            a = torch.linspace(-4, 4, 2 * 7 * 5 * 7).reshape(2, 7, 5, 7).to(dtype)
+            x = a.to(npu)
+            pointer = x.data_ptr()
+            out = F.silu(x, inplace=True)
+            assert out is x and x.data_ptr() == pointer
+            close(out, F.silu(a), 2)
+            for channels in (8, 7):
+                a = (torch.randn(2, channels, 13, 11, generator=gen(channels)) * 0.5).to(dtype)
+                x = a.to(npu)
+                p, q = torch.split(x, [channels // 2, channels - channels // 2], 1)
+                rp, rq = torch.split(a.clone(), [channels // 2, channels - channels // 2], 1)
+                F.silu(q, inplace=True)
+                F.silu(rq, inplace=True)
+                z = torch.cat((p, torch.add(q, q)), 1)
+                close(z, torch.cat((rp, torch.add(rq, rq)), 1), 2)
+
+
+def test_aten_routes_and_rejects(npu):
+    """verify_aten.py:119-147: inherited ops and 'thin aten' rejections."""
+    with torch.inference_mode():
+        a = torch.randn(1, 7, 5, 7, generator=gen(1))
+        an = a.to(npu)
+        close(torch.softmax(an, 1), torch.softmax(a, 1), 0)
+        assert bits_equal(torch.cat(an.split([3, 4], 1), 1).cpu(), a)
+        close(torch.sigmoid(an), torch.sigmoid(a), 0)
+        close(F.silu(an), F.silu(a), 0)
+        close(an + torch.ones(1, 7, 1, 1).to(npu), a + 1, 0)
+        assert bits_equal(F.interpolate(an, scale_factor=2, mode="nearest").cpu(),
+                          F.interpolate(a, scale_factor=2, mode="nearest"))
+        assert bits_equal(torch.ops.aten.upsample_nearest2d.vec(an, None, [2.0, 2.0]).cpu(),
+                          F.interpolate(a, scale_factor=2, mode="nearest"))
+        assert torch.arange(8, device="npu").cpu().tolist() == list(range(8))
+        assert torch.full((2, 3), 2.0, device="npu").cpu().eq(2).all()
+        assert torch.zeros(4, device="npu").cpu().eq(0).all()
+        assert torch.tensor(1.5).to("npu").item() == 1.5
+        for name, op in (("conv", lambda: F.conv2d(an, torch.randn(3, 7, 3, 3).to(npu))),
+                         ("pool", lambda: F.max_pool2d(an, 5, 1, 2)),
+                         ("nearest-3x", lambda: F.interpolate(an, scale_factor=3, mode="nearest"))):
+            with pytest.raises(RuntimeError, match="thin aten"):
+                op()
+
+
+def test_thin_backend_namespace(npu):
+    """verify_all.py:59-126: thin_backend.add (fp32), sigmoid, upsample, Meta."""
+    with torch.inference_mode():
+        for size in (5000, 65537, 1, 2049, 0):
+            a, b = torch.randn(size), torch.randn(size)
+            close(torch.ops.thin_backend.add(a.to(npu), b.to(npu)), a + b, 0)
+        for dtype in (torch.float32, torch.float16):
+            for size in (1, 5000, 65537):
+                x = torch.linspace(-8, 8, size, dtype=dtype)
+                close(torch.ops.thin_backend.sigmoid(x.to(npu)), torch.sigmoid(x), 2)
+            for shape in ((1, 2, 5, 7), (2, 3, 13, 11), (1, 64, 40, 40)):
+                x = torch.randn(shape).to(dtype)
+                assert bits_equal(torch.ops.thin_backend.upsample_nearest2d(x.to(npu)).cpu(),
+                                  F.interpolate(x, scale_factor=2, mode="nearest"))
+        for op, args in (("add", (torch.empty(5, device="meta"), torch.empty(5, device="meta"))),
+                         ("sigmoid", (torch.empty(7, device="meta"),)),
+                         ("upsample_nearest2d", (torch.empty(1, 16, 8, 8, device="meta"),))):
+            assert getattr(torch.ops.thin_backend, op)(*args).device.type == "meta"
+            for key in ("PrivateUse1", "AutogradPrivateUse1", "Meta"):
+                assert torch._C._dispatch_has_kernel_for_dispatch_key("thin_backend::" + op, key)
+
+
+def expression(x):
+    return torch.sigmoid((x + x) * 0.5)
+
+
+def test_graph_contract(npu):
+    """verify_graph.py:14-69 restated."""
+    from thin_backend.graph import CapturedForward
+    with torch.inference_mode():
+        x = torch.linspace(-2, 2, 2048).to(npu)
+        graph = CapturedForward(expression, x)
+        expected = expression(x).cpu()
+        for _ in range(5):
+            assert torch.equal(graph.replay().cpu(), expected)
+        other = torch.linspace(1, 3, 2048).to(npu)
+        assert torch.equal(graph(other).cpu(), expression(other).cpu())
+        with pytest.raises(ValueError):
+            graph(torch.empty(32, device="npu"))
+        errors = []
+
+        def wrong_thread():
+            for call in (graph.replay, lambda: graph(x)):
+                try:
+                    call()
+                except RuntimeError as error:
+                    errors.append(str(error))
+        t = threading.Thread(target=wrong_thread)
+        t.start()
+        t.join()
+        assert len(errors) == 2 and all("creating thread/stream" in e for e in errors)
+        second = CapturedForward(expression, x)
+        retained = graph.outputs
+        graph.close()
+        graph.close()
+        assert torch.equal(retained.cpu(), expression(other).cpu())
+        assert torch.equal(second.replay().cpu(), expected)
+        second.close()
+        with pytest.raises(RuntimeError, match="Device-to-host"):
+            CapturedForward(lambda value: value.cpu(), x)
+        graph = CapturedForward(expression, x)
+        retained = graph.outputs
+        del graph
+        assert torch.equal(retained.cpu(), expected)
+
+
+def test_frozen_graph(npu):
+    from blocked_graph import FrozenGraph
+
+    class Pilot:
+        calls = 0
+
+        def validate(self):
+            Pilot.calls += 1
+
+    pilot = Pilot()
+    with torch.inference_mode():
+        x = torch.linspace(-2, 2, 4096).half().to(npu)
+        g = FrozenGraph(pilot, expression, x)
+        assert torch.equal(g.replay().cpu(), expression(x).cpu())
+        y = torch.linspace(0, 1, 4096).half().to(npu)
+        assert torch.equal(g(y).cpu(), expression(y).cpu())
+        assert Pilot.calls == 3
+        g.close()
+
+
+def test_cat_plan_capture_changed_input(npu):
+    """verify_cat_plan.py:42-50: split -> cat captured, replayed with new inputs."""
+    from thin_backend.graph import CapturedForward
+    with torch.inference_mode():
+        for dtype in (torch.float16, torch.float32):
+            for count in (2, 6, 9, 17):
+                x = torch.randn(1, count * 2, 20, 20, 16, generator=gen(count)).to(dtype)
+                graph = CapturedForward(lambda v: torch.cat(v.split(2, 1), 1), x.to(npu))
+                for scale in (1, -0.75, 0.5):
+                    changed = x * scale
+                    assert bits_equal(graph(changed.to(npu)).cpu(), changed)
+                graph.close()
+
+
+def test_strided_binary_eager_equals_capture(npu):
+    """verify_strided_binary.py / verify_narrow_binary.py: eager == capture bitwise."""
+    from thin_backend.graph import CapturedForward
+    with torch.inference_mode():
+        full = torch.randn(1, 3, 44, 76, 16, generator=gen(2931)).half().to(npu)
+        grid = torch.randn(44, 76, 2, generator=gen(5)).half().to(npu)
+        scalar = torch.tensor(2, dtype=torch.float16).to(npu)
+        cases = [(full[..., :2], scalar), (full[..., 2:4], grid), (full[:, :1, ..., :2], full[..., :1]),
+                 (full[..., 1:9], scalar)]
+        for x, y in cases:
+            for op in ("add", "sub", "mul", "div"):
+                run = lambda _=None, x=x, y=y, op=op: getattr(torch, op)(x, y)
+                eager = run().cpu()
+                ref = getattr(torch, op)(x.cpu(), y.cpu())
+                assert_ulp(eager, ref, 0)
+                graph = CapturedForward(run, x)
+                assert bits_equal(graph.replay().cpu(), eager)
+                graph.close()
+
+
+def test_dfl_softmax_capture(npu):
+    """verify_dfl_softmax.py:25-52: the [B,16,4,A] DFL view via aten::_softmax,
+    eager within tolerance and capture bitwise x3."""
+    from thin_backend.graph import CapturedForward
+    with torch.inference_mode():
+        for width in (80, 8400):
+            cpu = (torch.randn(2, 4, 16, width, generator=gen(width)) * 3).half()
+            view = lambda t: t.transpose(1, 2)
+            forward = lambda value: torch.ops.aten._softmax.default(view(value), 1, False)
+            dev = cpu.to(npu)
+            eager = forward(dev).cpu()
+            assert_rel(eager, rd.softmax_rounded(view(cpu), 1), 1e-3, f"dfl {width}")
+            graph = CapturedForward(forward, dev)
+            for _ in range(3):
+                assert bits_equal(graph.replay().cpu(), eager)
+            graph.close()
+
+
+def test_flow_ops(npu):
+    """thin_native_flow.upsample / pack_input, thin_blocked.pack / unpack."""
+    with torch.inference_mode():
+        for c1, h, w, n in ((16, 20, 20, 1), (2, 13, 17, 1), (8, 40, 40, 3)):
+            bits = random_bits16((n, c1, h, w, 16), c1 + h)
+            assert bits_equal(torch.ops.thin_native_flow.upsample(bits.to(npu)).cpu(), mv.upsample2x_blocked(bits))
+        x = random_bits16((1, 3, 32, 32), 3)
+        assert bits_equal(torch.ops.thin_native_flow.pack_input(x.to(npu)).cpu(), mv.pack_blocked(x))
+        x = random_bits16((2, 64, 20, 20), 4)
+        y = torch.ops.thin_blocked.pack(x.to(npu))
+        assert bits_equal(y.cpu(), mv.pack_blocked(x))
+        assert bits_equal(torch.ops.thin_blocked.unpack(y).cpu(), x)
+        with pytest.raises(RuntimeError, match="not provided"):
+            torch.ops.thin_native_flow.maxpool(y, 5)
+
+
+def test_fused_ops(npu):
+    with torch.inference_mode():
+        x = to_blocked(normal16((2, 64, 40, 40), 1))
+        y = to_blocked(normal16((2, 64, 40, 40), 2))
+        got = torch.ops.thin_fused.silu_add(x.to(npu), y.to(npu)).cpu()
+        assert ulp_ok(got, ew.silu_add(x, y))
+        s = to_blocked((torch.rand(1, 64, 1, 1, generator=gen(3)) + 0.5).half())
+        b = to_blocked((torch.randn(1, 64, 1, 1, generator=gen(4)) * 0.1).half())
+        assert_ulp(torch.ops.thin_fused.affine_silu(x.to(npu), s.to(npu), b.to(npu)).cpu(), ew.affine_silu(x, s, b), 2)
+        up = to_blocked(normal16((2, 64, 20, 20), 5))
+        assert bits_equal(torch.ops.thin_fused.upsample_cat([up.to(npu), x.to(npu)], [1, 0]).cpu(),
+                          mv.upsample_cat_blocked([up, x], [True, False]))
+        logits = normal16((2, 64, 8400), 6, std=3.0)
+        assert_rel(torch.ops.thin_fused.dfl_expect(logits.to(npu)).cpu(), rd.dfl_expect(logits, torch.float32), 1e-3)
+
+
+def ulp_ok(got, ref):
+    from oracle.numerics import ulp_report
+    rep = ulp_report(got, ref)
+    return rep["nan_match"] and rep["exact"] > 0.999 * rep["finite"]
+
+
+def test_detection_select_eager_and_capture(npu):
+    """verify_selection_flow.py:229-265: production == trace output, eager ==
+    capture bitwise, changed-input replay bitwise, stages vs the oracle."""
+    from tests.selection_fixtures import c5_selection_input
+    with torch.inference_mode():
+        x = c5_selection_input()
+        base = x.transpose(1, 2).contiguous()
+        dev = base.to(npu)
+        view = lambda t: t.transpose(1, 2)
+        out = torch.ops.thin_native_flow.detection_select(view(dev), 300, False)
+        ref = sel.select(x, 300, False)
+        assert bits_equal(out.cpu(), ref["output"])
+        trace = torch.ops.thin_native_flow.detection_select_trace(view(dev), 300, False)
+        assert len(trace) == 8 and bits_equal(trace[0].cpu(), ref["output"])
+        for got, name in zip(trace[1:], sel.TRACE_NAMES[1:]):
+            assert bits_equal(got.cpu(), ref[name].to(got.dtype)), name
+        graph = torch.classes.thin_backend.RuntimeGraph()
+        graph.begin()
+        captured = torch.ops.thin_native_flow.detection_select(view(dev), 300, False)
+        graph.end()
+        graph.replay()
+        assert bits_equal(captured.cpu(), out.cpu())
+        changed = -base
+        dev.copy_(changed.to(npu))
+        changed_eager = torch.ops.thin_native_flow.detection_select(view(dev), 300, False).cpu()
+        assert bits_equal(changed_eager, sel.select(view(changed), 300, False)["output"])
+        graph.replay()
+        assert bits_equal(captured.cpu(), changed_eager)
+        graph.close()
