@@ -200,7 +200,9 @@ typedef struct thin_select_trace {
   void* labels;
 } thin_select_trace;
 
-/* Bytes of device workspace thin_detection_select needs for these sizes. */
+/* Bytes of device workspace thin_detection_select needs for these sizes.
+ * Replaces the intermediate tensors the reference allocates per call
+ * (selection_flow.cpp:445-466: maxima, gathered, indices, values, records). */
 size_t thin_detection_select_workspace(int64_t batches, int64_t anchors, int64_t classes,
                                        int64_t max_det, int32_t agnostic);
 

@@ -310,20 +310,26 @@ at::Tensor affine_silu(const at::Tensor& x, const at::Tensor& s, const at::Tenso
   after_launch();
   return out;
 }
-at::Tensor upsample_cat(at::TensorList xs, at::IntArrayRef upsample) {
+// Output sizes of upsample_cat: H, W of the first input taken as is, or twice
+// those of the first input when every input is upsampled.
+std::vector<int64_t> upsample_cat_sizes(at::TensorList xs, at::IntArrayRef upsample) {
   TORCH_CHECK(!xs.empty() && xs.size() == upsample.size(), "upsample_cat expects matching tensor and flag lists");
   const at::Tensor* ref = nullptr;
+  int64_t c1 = 0;
   for (size_t i = 0; i < xs.size(); ++i) {
-    inference(xs[i], "thin_fused.upsample_cat");
     TORCH_CHECK(xs[i].dim() == 5, "upsample_cat expects NC1HWC0 tensors");
     if (!ref && !upsample[i]) ref = &xs[i];
+    c1 += xs[i].size(1);
   }
   const int64_t scale = ref ? 1 : 2;
   if (!ref) ref = &xs[0];
-  int64_t c1 = 0;
-  for (const auto& t : xs) c1 += t.size(1);
-  select(ref->device());
-  auto out = at::empty({ref->size(0), c1, ref->size(2) * scale, ref->size(3) * scale, ref->size(4)}, ref->options());
+  return {ref->size(0), c1, ref->size(2) * scale, ref->size(3) * scale, ref->size(4)};
+}
+at::Tensor upsample_cat(at::TensorList xs, at::IntArrayRef upsample) {
+  for (const auto& t : xs) inference(t, "thin_fused.upsample_cat");
+  auto sizes = upsample_cat_sizes(xs, upsample);
+  select(xs[0].device());
+  auto out = at::empty(sizes, xs[0].options());
   if (!out.numel()) return out;
   std::vector<thin_desc> ds;
   std::vector<int32_t> up;
@@ -347,6 +353,25 @@ at::Tensor dfl_expect(const at::Tensor& x, bool fp32_output) {
   check(thin_dfl_expect(&xd, &od, stream()), "thin dfl_expect");
   after_launch();
   return out;
+}
+
+// Meta kernels of thin_fused: the shapes and dtypes of the device kernels.
+at::Tensor silu_add_meta(const at::Tensor& x, const at::Tensor& y) {
+  TORCH_CHECK(float_type(x) && x.scalar_type() == y.scalar_type(), "silu_add requires matching float16/float32");
+  return at::empty(at::infer_size(x.sizes(), y.sizes()), x.options());
+}
+at::Tensor affine_silu_meta(const at::Tensor& x, const at::Tensor& s, const at::Tensor& b) {
+  TORCH_CHECK(float_type(x) && s.scalar_type() == x.scalar_type() && b.scalar_type() == x.scalar_type(),
+              "affine_silu requires matching float16/float32");
+  return at::empty(x.sizes(), x.options());
+}
+at::Tensor upsample_cat_meta(at::TensorList xs, at::IntArrayRef upsample) {
+  return at::empty(upsample_cat_sizes(xs, upsample), xs[0].options());
+}
+at::Tensor dfl_expect_meta(const at::Tensor& x, bool fp32_output) {
+  TORCH_CHECK(x.scalar_type() == at::kHalf && x.dim() == 3 && x.size(1) == 64,
+              "dfl_expect expects float16 box logits [N,64,A]");
+  return at::empty({x.size(0), 4, x.size(2)}, x.options().dtype(fp32_output ? at::kFloat : at::kHalf));
 }
 
 }  // namespace thin_ops
@@ -409,4 +434,11 @@ TORCH_LIBRARY_IMPL(thin_fused, PrivateUse1, m) {
 TORCH_LIBRARY_IMPL(thin_fused, AutogradPrivateUse1, m) {
   for (const char* name : {"silu_add", "affine_silu", "upsample_cat", "dfl_expect"})
     m.impl(name, torch::CppFunction::makeFallthrough());
+}
+
+TORCH_LIBRARY_IMPL(thin_fused, Meta, m) {
+  m.impl("silu_add", TORCH_FN(thin_ops::silu_add_meta));
+  m.impl("affine_silu", TORCH_FN(thin_ops::affine_silu_meta));
+  m.impl("upsample_cat", TORCH_FN(thin_ops::upsample_cat_meta));
+  m.impl("dfl_expect", TORCH_FN(thin_ops::dfl_expect_meta));
 }
