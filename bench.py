@@ -397,7 +397,7 @@ def main():
     achieved = algo / dom_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": dominant_traffic(),
-                "kernel": "affine_silu_blocked_kernel<2, true> (thin_affine_silu)",
+                "kernel": "affine_silu_flat_kernel<true, true> (thin_affine_silu)",
                 "launch": f"N=32 C,H,W={C2_SHAPES[0]}: {algo} algorithmic bytes, avg {dom_s * 1e6:.2f} us",
                 "traffic_note": "HBM bytes per launch = FETCH_SIZE x fetch factor + WRITE_SIZE x write factor, "
                                 "factors from a plain 16-byte copy of the same tensor (rocprofv3 --pmc, "

@@ -191,6 +191,45 @@ def test_affine_silu_c2(gpu, n, chw):
     assert_ulp(got, ew.affine_silu(xn, sn, bn), 2, f"affine_silu narrowed {n} {chw}")
 
 
+@pytest.mark.parametrize("case", ["per_image_scale", "channel_stride", "wide_c1", "tiny_planes",
+                                  "narrowed_out", "strided_scale", "n1_offset"])
+def test_affine_silu_layouts(gpu, case):
+    """Every NC1HWC0 layout the fused kernel accepts, flat-span and per-plane
+    forms alike, against the op-by-op fp16 chain; outputs written through a
+    view leave the rest of their parent untouched."""
+    from thintnpu_amd import capi
+    n, c, h, w = {"per_image_scale": (3, 64, 5, 7), "channel_stride": (2, 128, 6, 10),
+                  "wide_c1": (2, 4096, 2, 3), "tiny_planes": (5, 16, 1, 1), "narrowed_out": (4, 96, 9, 11),
+                  "strided_scale": (2, 64, 8, 8), "n1_offset": (1, 256, 20, 20)}[case]
+    x, s, b = c2_inputs(n, c, h, w, seed=len(case))
+    if case == "per_image_scale":
+        s = (torch.rand((n, c // 16, 1, 1, 16), generator=gen(5)) + 0.5).half()
+        b = (torch.randn((n, c // 16, 1, 1, 16), generator=gen(6)) * 0.1).half()
+    xv = lambda t: t  # noqa: E731
+    sv = lambda t: t  # noqa: E731
+    if case == "channel_stride":
+        xv = sv = lambda t: t[:, ::2]  # noqa: E731
+    if case == "strided_scale":
+        s2 = (torch.rand((1, c // 8, 1, 1, 16), generator=gen(7)) + 0.5).half()
+        b2 = (torch.randn((1, c // 8, 1, 1, 16), generator=gen(8)) * 0.1).half()
+        s, b = s2, b2
+        sv = lambda t: t[:, ::2]  # noqa: E731
+    if case == "n1_offset":
+        xv = sv = lambda t: t[:, 3:11]  # noqa: E731
+    xg, sg, bg = xv(x.to(gpu)), sv(s.to(gpu)), sv(b.to(gpu))
+    ref = ew.affine_silu(xv(x), sv(s), sv(b).expand_as(sv(s)))
+    if case == "narrowed_out":
+        fill = random_bits16((n, c // 16 + 2, h, w, 16), 11)
+        parent = fill.to(gpu)
+        capi.affine_silu(xg, sg, bg, out=parent[:, 2:])
+        got = parent.cpu()
+        assert_ulp(got[:, 2:], ref, 2, case)
+        assert bits_equal(got[:, :2], fill[:, :2])
+        return
+    got = capi.affine_silu(xg, sg, bg).cpu()
+    assert_ulp(got, ref, 2, case)
+
+
 def test_copy_bit_exact(gpu):
     from thintnpu_amd import capi
     raw = random_bits16((3, 32, 48), 913)

@@ -162,8 +162,10 @@ struct alignas(16) VecT {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16-byte store; NT selects a streaming (non-temporal) store for outputs too
-// large to stay cache-resident for their consumer -- on gfx950 it lifts a
-// plain HBM copy from ~5.1 to ~6.6 TB/s.
+// large to stay cache-resident for their consumer.  Measured on gfx950 over a
+// 1 GB rotation (Infinity Cache defeated), a 52 MB copy moves 5.5 TB/s with
+// cached loads and stores, 5.5-5.7 with streaming stores and 5.7-6.0 with
+// streaming loads and stores.
 template <bool NT, typename W>
 __device__ __forceinline__ void store16(void* dst, const W& w) {
   static_assert(sizeof(W) == 16, "16-byte store");
@@ -181,11 +183,12 @@ __device__ __forceinline__ W load16(const void* src) {
 }
 
 // Outputs of at least this many bytes are written with streaming
-// (non-temporal) stores; smaller ones keep cached stores so that the next
-// kernel finds them in L2 / MALL.  Measured on gfx950 with the Infinity Cache
-// defeated: 256-thread blocks with two 16-byte vectors per thread, cached
-// loads and streaming stores beat 1024-thread blocks with eight vectors and
-// non-temporal loads for every kernel here except a bare copy.
+// (non-temporal) stores, and inputs read once in full at that size are read
+// with streaming loads; smaller ones stay cached so that producer and consumer
+// kernels meet in L2 / MALL.  Operands re-read across the grid (broadcast
+// scale/bias) always use cached loads.  On gfx950, 256-thread blocks with two
+// 16-byte vectors per thread and one tile per block measured best for every
+// kernel here (1024-thread blocks and 4-8 vectors per thread were slower).
 constexpr int64_t kStreamingStoreBytes = (int64_t)16 << 20;
 
 // Unit offsets for the vector kernel; ND == 1 means every operand is flat
@@ -300,6 +303,46 @@ __global__ __launch_bounds__(kThreads) void map_scalar_kernel(MapPlan<NIN> p) {
   }
 }
 
+// Dense form: every operand is one contiguous run (one coalesced dim, unit
+// stride), so unit u lives at element u * V of each operand.  One tile of
+// kThreads * U vectors per block and no per-operand load-mode branches; NT
+// streams both the loads and the stores.  The cache policy is a template
+// parameter so that the compiler emits the non-temporal forms.
+template <typename T, int V, int NIN, int U, bool NT, class Op>
+__global__ __launch_bounds__(kThreads) void map_dense_kernel(MapPlan<NIN> p) {
+  const uint32_t tile = blockIdx.x * (kThreads * U);
+  VecT<T, V> raw[U][NIN];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t unit = tile + u * kThreads + threadIdx.x;
+    if (unit < p.units) {
+#pragma unroll
+      for (int k = 0; k < NIN; ++k)
+        raw[u][k] = load16<NT, VecT<T, V>>(static_cast<const T*>(p.in[k]) + (size_t)unit * V);
+    }
+  }
+  const Op op;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t unit = tile + u * kThreads + threadIdx.x;
+    if (unit >= p.units) break;
+    T* dst = static_cast<T*>(p.out) + (size_t)unit * V;
+    if constexpr (std::is_same<Op, OpCopy>::value) {
+      store16<NT>(dst, raw[u][0]);
+    } else {
+      VecT<T, V> r;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        T lane[NIN];
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) lane[k] = raw[u][k].v[j];
+        r.v[j] = op.template operator()<T, NIN>(lane, p.pa, p.pb);
+      }
+      store16<NT>(dst, r);
+    }
+  }
+}
+
 // ------------------------------------------------------------ NC1HWC0 affine
 
 // Per-channel affine + SiLU on NC1HWC0 fp16 planes.  A plane (n, c1) is H*W*16
@@ -354,6 +397,100 @@ __global__ __launch_bounds__(kThreads) void affine_silu_blocked_kernel(AffinePla
   }
 }
 
+// Flat form of the same op for the common layout: within one image the C1
+// planes of x and of out are contiguous (full tensors and C2f channel slices
+// x[:, a:b]), and scale/bias do not vary with n.  The work is then rows (images)
+// x one contiguous span of C1 * H * W * 2 vectors, split into one tile of
+// kThreads * 2 vectors per block with no per-plane loop; the channel of a
+// vector is its span offset / plane size and its C0 half the offset's parity.
+// The image's 2 * C1 scale and bias vectors are staged once per block in LDS.
+constexpr uint32_t kFlatMaxC1 = 128;
+
+struct AffineFlatPlan {
+  const h8v* x;
+  h8v* out;
+  const h8v* s;      // channel 0, C0 lanes 0-7; lanes 8-15 follow
+  const h8v* b;
+  uint32_t total;    // rows * span vectors
+  FastDiv span;      // vectors per row
+  FastDiv plane;     // vectors per (n, c1) plane
+  uint32_t x_row, o_row;  // row strides in vectors
+  uint32_t s_c1, b_c1;    // channel strides in vectors
+  uint32_t c1;            // channel blocks per row
+};
+
+template <bool NTL, bool NTS>
+__global__ __launch_bounds__(kThreads) void affine_silu_flat_kernel(AffineFlatPlan p) {
+  constexpr int U = 2;
+  __shared__ h8v sb[2][2 * kFlatMaxC1];
+  for (uint32_t i = threadIdx.x; i < 2 * p.c1; i += kThreads) {
+    sb[0][i] = p.s[(i >> 1) * p.s_c1 + (i & 1u)];
+    sb[1][i] = p.b[(i >> 1) * p.b_c1 + (i & 1u)];
+  }
+  __syncthreads();
+  const uint32_t tile = blockIdx.x * (kThreads * U);
+  h8v v[U];
+  uint32_t oo[U], q[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tile + u * kThreads + threadIdx.x;
+    if (i < p.total) {
+      const uint32_t row = p.span.div(i);
+      const uint32_t col = i - row * p.span.d;
+      oo[u] = row * p.o_row + col;
+      q[u] = p.plane.div(col) * 2 + (col & 1u);
+      const h8v* src = p.x + row * p.x_row + col;
+      v[u] = NTL ? __builtin_nontemporal_load(src) : *src;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tile + u * kThreads + threadIdx.x;
+    if (i >= p.total) break;
+    h8v t = v[u] * sb[0][q[u]];  // packed fp16, correctly rounded
+    t = t + sb[1][q[u]];
+    h8v r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (_Float16)silu_f<_Float16>((float)t[j]);
+    store16<NTS>(p.out + oo[u], r);
+  }
+}
+
+bool try_affine_flat(const thin_desc* x, const thin_desc* sc, const thin_desc* b, const thin_desc* out,
+                     hipStream_t stream) {
+  const int64_t n = x->sizes[0], c1 = x->sizes[1];
+  const int64_t plane_elems = x->sizes[2] * x->sizes[3] * 16;
+  if (c1 > (int64_t)kFlatMaxC1) return false;
+  if (c1 > 1 && (x->strides[1] != plane_elems || out->strides[1] != plane_elems)) return false;
+  if (n > 1 && (sc->strides[0] != 0 || b->strides[0] != 0)) return false;
+  const int64_t plane_vecs = plane_elems / 8;
+  const int64_t span = c1 * plane_vecs;
+  const int64_t total = n * span;
+  const int64_t x_row = n > 1 ? x->strides[0] / 8 : 0, o_row = n > 1 ? out->strides[0] / 8 : 0;
+  const int64_t lim = ((int64_t)1 << 32) - 1;
+  if (total >= ((int64_t)1 << 31) || x_row < 0 || o_row < 0 || (n - 1) * x_row + span > lim ||
+      (n - 1) * o_row + span > lim)
+    return false;
+  AffineFlatPlan p;
+  p.x = static_cast<const h8v*>(x->data);
+  p.out = static_cast<h8v*>(out->data);
+  p.s = static_cast<const h8v*>(sc->data);
+  p.b = static_cast<const h8v*>(b->data);
+  p.total = (uint32_t)total;
+  p.span = FastDiv::make((uint32_t)span);
+  p.plane = FastDiv::make((uint32_t)plane_vecs);
+  p.x_row = (uint32_t)x_row;
+  p.o_row = (uint32_t)o_row;
+  p.s_c1 = (uint32_t)(sc->strides[1] / 8);
+  p.b_c1 = (uint32_t)(b->strides[1] / 8);
+  p.c1 = (uint32_t)c1;
+  const uint32_t grid = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
+  const bool nt = total * 16 >= kStreamingStoreBytes;
+  if (nt) hipLaunchKernelGGL((affine_silu_flat_kernel<true, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((affine_silu_flat_kernel<false, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+  return true;
+}
+
 // Returns true and launches when x/s/b/out have the NC1HWC0 per-channel form.
 bool try_affine_blocked(const thin_desc* x, const thin_desc* sc, const thin_desc* b,
                         const thin_desc* out, hipStream_t stream) {
@@ -368,6 +505,7 @@ bool try_affine_blocked(const thin_desc* x, const thin_desc* sc, const thin_desc
            reinterpret_cast<uintptr_t>(d->data) % 16 == 0 && d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0;
   };
   if (!dense_plane(x) || !dense_plane(out) || !per_channel(sc) || !per_channel(b)) return false;
+  if (try_affine_flat(x, sc, b, out, stream)) return true;
   const int64_t planes = x->sizes[0] * x->sizes[1];
   const int64_t plane_vecs = h * w * 2;
   if (planes >= ((int64_t)1 << 31) || plane_vecs >= ((int64_t)1 << 30)) return false;
@@ -407,6 +545,18 @@ constexpr int kUnroll = 2;
 template <typename T, int NIN, int ND, class Op>
 void launch_plan(const MapPlan<NIN>& p, bool vec, bool nt, hipStream_t stream) {
   constexpr int V = 16 / (int)sizeof(T);
+  if constexpr (ND == 1) {
+    bool dense = vec && p.out_mode == kVec;
+    for (int k = 0; k < NIN; ++k) dense = dense && p.in_mode[k] == kVec;
+    if (dense) {
+      const uint32_t grid = (p.units + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+      if (nt) hipLaunchKernelGGL((map_dense_kernel<T, V, NIN, kUnroll, true, Op>), dim3(grid), dim3(kThreads), 0,
+                                 stream, p);
+      else hipLaunchKernelGGL((map_dense_kernel<T, V, NIN, kUnroll, false, Op>), dim3(grid), dim3(kThreads), 0,
+                              stream, p);
+      return;
+    }
+  }
   if (vec) {
     if (nt) {
       uint32_t grid = grid_for(p.units, kThreads, kUnroll, 256u * 64u);

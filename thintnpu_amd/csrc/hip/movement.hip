@@ -27,6 +27,13 @@ __device__ __forceinline__ void st16(void* dst, u32x4 v) {
   else *reinterpret_cast<u32x4*>(dst) = v;
 }
 __device__ __forceinline__ u32x4 ld16(const void* src) { return *reinterpret_cast<const u32x4*>(src); }
+// Streaming (non-temporal) load for data read exactly once by a launch that
+// also streams its stores.
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16s(const void* src) {
+  if (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+  return *reinterpret_cast<const u32x4*>(src);
+}
 
 // Large outputs (>= kStreamingStoreBytes) are written with streaming stores;
 // loads stay cached (see the launch-shape note in elementwise.hip).
@@ -99,7 +106,7 @@ __global__ __launch_bounds__(BS) void cat_kernel(CatPlan p) {
   for (int u = 0; u < U; ++u) {
     const int64_t k = base + u * BS + threadIdx.x;
     if (k < n) {
-      if constexpr (sizeof(W) == 16) v[u] = __builtin_bit_cast(W, ld16(src + k));
+      if constexpr (sizeof(W) == 16) v[u] = __builtin_bit_cast(W, ld16s<NT>(src + k));
       else v[u] = src[k];
     }
   }
@@ -223,7 +230,7 @@ __global__ __launch_bounds__(BS) void plane_kernel(PlanePlan p) {
         // each source vector feeds four outputs: keep it cacheable
         v[u] = ld16(src + (size_t)((oy >> 1) * in_row + (ox >> 1) * p.vpp + k) * 16);
       } else {
-        v[u] = ld16(src + (size_t)o * 16);
+        v[u] = ld16s<NT>(src + (size_t)o * 16);
       }
     }
 #pragma unroll
@@ -417,7 +424,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackPlan p) {
       const uint32_t c = k / (kTile / 8), j = k % (kTile / 8);
       const uint32_t ch = cb * 16 + c;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (ch < p.channels) v = ld16(p.x + n * p.x_n + (int64_t)ch * p.x_c + pix0 + j * 8);
+      if (ch < p.channels) v = ld16s<NT>(p.x + n * p.x_n + (int64_t)ch * p.x_c + pix0 + j * 8);
       const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
       for (int q = 0; q < 8; ++q) tile[c][j * 8 + q] = h[q];
