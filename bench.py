@@ -102,11 +102,12 @@ def time_launches(launch, sets, iters, rounds=5):
 
 
 # rocprofv3 --pmc readings (KiB per dispatch, median over the dispatches) of the
-# dominant kernel, affine_silu_blocked_kernel at N=32 (128,80,80), and of the
-# plain copy map_vec_kernel<OpCopy> over the same [32,8,80,80,16] fp16 tensor
-# (104857600 B read + written), from `bench.py --profile dominant|copy --iters 20`.
-PMC_KIB = {"dominant": {"FETCH_SIZE": 25622.0, "WRITE_SIZE": 51200.875},
-           "copy": {"FETCH_SIZE": 25620.5, "WRITE_SIZE": 51253.625}}
+# dominant kernel, affine_silu_flat_kernel at N=32 (128,80,80), and of the dense
+# copy map_dense_kernel<OpCopy> over the same [32,8,80,80,16] fp16 tensor
+# (104857600 B read + written), from `bench.py --profile dominant|copy --iters 20`
+# (profiles/affine_silu_flat_n32_128x80x80_pmc.md).
+PMC_KIB = {"dominant": {"FETCH_SIZE": 25619.0, "WRITE_SIZE": 51200.375},
+           "copy": {"FETCH_SIZE": 25610.0, "WRITE_SIZE": 51250.625}}
 COPY_BYTES_EACH_WAY = 52428800
 
 
@@ -401,7 +402,7 @@ def main():
                 "launch": f"N=32 C,H,W={C2_SHAPES[0]}: {algo} algorithmic bytes, avg {dom_s * 1e6:.2f} us",
                 "traffic_note": "HBM bytes per launch = FETCH_SIZE x fetch factor + WRITE_SIZE x write factor, "
                                 "factors from a plain 16-byte copy of the same tensor (rocprofv3 --pmc, "
-                                "profiles/affine_silu_blocked_n32_128x80x80_pmc.txt)"}
+                                "profiles/affine_silu_flat_n32_128x80x80_pmc.md)"}
     del sets
 
     ops = []
