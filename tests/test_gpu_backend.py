@@ -332,3 +332,60 @@ def test_detection_select_eager_and_capture(npu):
         graph.replay()
         assert bits_equal(captured.cpu(), changed_eager)
         graph.close()
+
+
+def test_region_contract_guards_frozen_graph(npu):
+    """RegionContract as FrozenGraph's pilot: replays while the region is
+    frozen, ValueError once a parameter changes (blocked_graph.py:4-23,
+    region_contract.py:5-28)."""
+    import torch.nn as nn
+    from blocked_graph import FrozenGraph
+    from region_contract import RegionContract
+
+    class Scale(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.register_buffer("s", torch.full((1, 4, 1, 1, 16), 0.5, dtype=torch.float16).to(npu))
+
+        def forward(self, x):
+            return F.silu(torch.mul(x, self.s))
+
+    with torch.no_grad():
+        m = nn.Sequential(Scale()).eval()
+        contract = RegionContract((m,))
+        x = normal16((1, 4, 8, 8, 16), 3).to(npu)
+        g = FrozenGraph(contract, m, x)
+        assert bits_equal(g.replay().cpu(), m(x).cpu())
+        m[0].s.copy_(m[0].s * 2)
+        with pytest.raises(ValueError, match="version"):
+            g.replay()
+        g.close()
+    with pytest.raises(ValueError, match="Expected fixed FP16 NPU"):
+        RegionContract((nn.Linear(2, 2),))
+
+
+def test_aten_trace_and_process_hygiene(npu, capfd, monkeypatch):
+    """THIN_ATEN_TRACE=1 logs each aten -> thin route (aten_adapter.cpp:25-29);
+    the process maps the native HIP libraries and spawns no children
+    (verify_ops.py:36-50)."""
+    import os
+    x = torch.linspace(-3, 3, 4096).half().to(npu)
+    monkeypatch.setenv("THIN_ATEN_TRACE", "1")
+    torch.sigmoid(x)
+    F.silu(x)
+    torch.ops.aten.upsample_nearest2d.vec(x.view(1, 4, 32, 32), None, [2.0, 2.0])
+    err = capfd.readouterr().err
+    for route in ("aten::sigmoid -> thin_unary(SIGMOID)", "aten::silu -> thin_unary(SILU)",
+                  "aten::upsample_nearest2d -> thin_upsample2x_nchw"):
+        assert f"THIN_ATEN {route} device=npu:0" in err
+    monkeypatch.delenv("THIN_ATEN_TRACE")
+    torch.sigmoid(x)
+    assert "THIN_ATEN" not in capfd.readouterr().err
+    maps = open("/proc/self/maps").read()
+    assert "libthin_hip.so" in maps and "libthin_backend.so" in maps
+    def parent(pid):
+        try:
+            return int(open(f"/proc/{pid}/stat").read().rsplit(") ", 1)[1].split()[1])
+        except (OSError, IndexError, ValueError):
+            return None
+    assert [p for p in os.listdir("/proc") if p.isdigit() and parent(p) == os.getpid()] == []

@@ -58,6 +58,7 @@ def build(verbose: bool = False) -> None:
     hip_libs = [f"-L{ROCM / 'lib'}", "-lamdhip64"]
     rpaths = ["-Wl,-rpath,$ORIGIN", "-Wl,-rpath,$ORIGIN/../thintnpu_amd", f"-Wl,-rpath,{base / 'lib'}",
               f"-Wl,-rpath,{ROCM / 'lib'}"]
+    guard = cf.ThreadPoolExecutor(1).submit(build_region_guard, verbose)
     for lib, srcs in LIBS.items():
         objs = [str(obj_dir / (s + ".o")) for s in srcs]
         extra = [] if lib == "libthin_backend.so" else [f"-L{OUT}", "-lthin_backend"]
@@ -65,6 +66,26 @@ def build(verbose: bool = False) -> None:
         _run([cxx, "-shared", "-fPIC", *objs, "-o", str(tmp), *extra, f"-L{HIP_LIB.parent}", "-lthin_hip",
               *torch_libs, *hip_libs, *rpaths])
         os.replace(tmp, OUT / lib)
+    guard.result()
+
+
+def build_region_guard(verbose: bool = False) -> Path:
+    """pybind11 extension thin_backend/_region_guard<EXT_SUFFIX> (host C++ only)."""
+    import sysconfig
+    base, abi = _torch_paths()
+    suffix = sysconfig.get_config_var("EXT_SUFFIX")
+    target = OUT / ("_region_guard" + suffix)
+    cxx = os.environ.get("CXX", "g++")
+    cmd = [cxx, "-std=c++17", "-O2", "-shared", "-fPIC", "-fvisibility=hidden", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           f"-I{sysconfig.get_paths()['include']}", f"-I{base / 'include'}",
+           f"-I{base / 'include' / 'torch' / 'csrc' / 'api' / 'include'}", "-Wno-deprecated-declarations",
+           str(TORCH_SRC / "region_guard.cpp"), "-o", str(target) + ".tmp", f"-L{base / 'lib'}", "-ltorch_python",
+           "-ltorch_cpu", "-ltorch", "-lc10", f"-Wl,-rpath,{base / 'lib'}"]
+    if verbose:
+        print(" ".join(cmd), file=sys.stderr)
+    _run(cmd)
+    os.replace(str(target) + ".tmp", target)
+    return target
 
 
 if __name__ == "__main__":
