@@ -170,13 +170,22 @@ def test_dfl_expect_views_and_specials(gpu):
     v = x.transpose(1, 2)  # [2,64,8400] with anchor stride 64
     got = capi.dfl_expect(x.to(gpu).transpose(1, 2)).cpu()
     assert_rel(got, rd.dfl_expect(v, torch.float32), 1e-3, "dfl transposed")
-    y = normal16((1, 64, 17), 7, std=3.0)
-    y[0, 3, 2] = float("nan")
-    y[0, 20, 5] = float("inf")
-    y[0, 32:48, 7] = float("-inf")
-    y[0, 48:64, 9] = 0
-    got = capi.dfl_expect(y.to(gpu)).cpu()
-    assert_rel(got, rd.dfl_expect(y, torch.float32), 1e-3, "dfl specials")
+    for width in (17, 18, 64):  # one-anchor and two-anchor thread forms
+        y = normal16((2, 64, width), 7 + width, std=3.0)
+        y[0, 3, 2] = float("nan")
+        y[0, 20, 5] = float("inf")
+        y[0, 20, 4] = float("inf")
+        y[0, 32:48, 7] = float("-inf")
+        y[0, 48:64, 9] = 0
+        y[1, 0:16, 10] = y[1, 0:16, 10] + 10000      # large shift
+        y[1, 16:32, 11] = y[1, 16:32, 11] - 10000
+        y[1, 32, 12], y[1, 47, 12] = 65504.0, -65504.0  # fp16 extremes in one side
+        y[1, 48:64, 13] = float("-inf")
+        y[1, 50, 13] = 1.0                            # one finite bin: expectation 2
+        for out_dtype in (torch.float16, torch.float32):
+            got = capi.dfl_expect(y.to(gpu), out_dtype).cpu()
+            assert_rel(got, rd.dfl_expect(y, out_dtype), 1e-3, f"dfl specials {width} {out_dtype}")
+        assert float(capi.dfl_expect(y.to(gpu)).cpu()[1, 3, 13]) == 2.0
 
 
 @pytest.mark.parametrize("n", [1, 32])

@@ -231,46 +231,65 @@ struct DflPlan {
   FastDiv div_avecs;
 };
 
+// The bin maximum only stabilises the exponentials, so it is taken without
+// NaN propagation (in packed fp16 for two anchors, where max is exact): a NaN
+// bin, a +inf bin (inf - inf) or an all -inf side (-inf - -inf) already makes
+// the sum, and so the result, NaN -- as CPU's softmax then expectation does.
+// FAST (fp16 output): e = exp2(x*log2e - m*log2e) as one fma (an error in the
+// common term m*log2e scales every e_i alike and cancels in w/s) and w * 1/s;
+// the fp32 output uses expf and an IEEE division.
 template <typename TO, int V, bool FAST>
 __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
+  static_assert(V == 1 || V == 2, "one or two anchors per thread");
   const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
   if (u >= p.units) return;
   const uint32_t side = p.div_avecs.div(u);
   const uint32_t a0 = (u - side * p.avecs) * V;
   const uint32_t n = side >> 2, sd = side & 3u;
   const _Float16* xp = p.x + n * p.xn + (int64_t)(sd * 16) * p.xc + (int64_t)a0 * p.xa;
-  struct alignas(V * 2 >= 16 ? 16 : 2) WI { _Float16 e[V]; };
-  WI bins[16];
+  typedef _Float16 hv __attribute__((ext_vector_type(2)));
+  _Float16 bins[16][V];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    if (V > 1) {
-      bins[i] = *reinterpret_cast<const WI*>(xp + i * p.xc);
+    if (V == 2) {
+      const hv b = *reinterpret_cast<const hv*>(xp + i * p.xc);
+      bins[i][0] = b[0];
+      bins[i][V - 1] = b[1];
     } else {
-      bins[i].e[0] = xp[i * p.xc];
+      bins[i][0] = xp[i * p.xc];
     }
   }
+  float m[V];
+  if (V == 2) {
+    hv mv = {bins[0][0], bins[0][V - 1]};
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mv = __builtin_elementwise_max(mv, (hv){bins[i][0], bins[i][V - 1]});
+    m[0] = (float)mv[0];
+    m[V - 1] = (float)mv[1];
+  } else {
+    m[0] = (float)bins[0][0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) m[0] = fmaxf(m[0], (float)bins[i][0]);
+  }
+  constexpr float kLog2e = 1.4426950408889634f;
   float r[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < 16; ++i) m = max_nan(m, (float)bins[i].e[j]);
+    const float ml = m[j] * kLog2e;
     float s = 0.f, w = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float e = expo<FAST>((float)bins[i].e[j] - m);
+      const float x = (float)bins[i][j];
+      const float e = FAST ? __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -ml)) : expf(x - m[j]);
       s += e;
       w += e * (float)i;
     }
-    r[j] = w / s;
+    r[j] = FAST ? w * __builtin_amdgcn_rcpf(s) : w / s;
   }
   TO* op = static_cast<TO*>(p.out) + n * p.on + (int64_t)sd * p.os + (int64_t)a0 * p.oa;
-  if (V > 1) {
-    struct alignas(V * sizeof(TO) >= 16 ? 16 : alignof(TO)) WO { TO e[V]; };
-    WO o;
-#pragma unroll
-    for (int j = 0; j < V; ++j) o.e[j] = (TO)r[j];
-    *reinterpret_cast<WO*>(op) = o;
+  if (V == 2) {
+    typedef TO ov __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<ov*>(op) = (ov){(TO)r[0], (TO)r[V - 1]};
   } else {
     op[0] = (TO)r[0];
   }
@@ -414,9 +433,12 @@ extern "C" thin_status thin_dfl_expect(const thin_desc* x, const thin_desc* out,
   const int64_t A = x->sizes[2];
   p.sides = (uint32_t)(x->sizes[0] * 4);
   const int esz = out->dtype == THIN_F32 ? 4 : 2;
-  constexpr int V = 8;
-  const bool vec = A % V == 0 && p.xa == 1 && p.oa == 1 && aligned(x->data, 16) && aligned(out->data, 16) &&
-                   (p.xn * 2) % 16 == 0 && (p.xc * 2) % 16 == 0 && (p.on * esz) % 16 == 0 && (p.os * esz) % 16 == 0;
+  // Two anchors per thread (4-byte loads): more waves than wider vectors, so
+  // the 32 exponentials per thread overlap the loads of other waves.
+  constexpr int V = 2;
+  const bool vec = A % V == 0 && p.xa == 1 && p.oa == 1 && aligned(x->data, 2 * V) &&
+                   aligned(out->data, esz * V) && p.xn % V == 0 && p.xc % V == 0 && p.on % V == 0 &&
+                   p.os % V == 0;
   const int v = vec ? V : 1;
   p.avecs = (uint32_t)(A / v);
   const uint64_t units = (uint64_t)p.sides * p.avecs;
