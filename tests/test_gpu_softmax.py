@@ -51,6 +51,9 @@ def test_softmax_reference_cases(gpu, dtype):
         ((2, 1000, 17), (1,)), ((3, 7, 1), (1,)),
         ((1, 4, 16, 8400), (1, 2)), ((1, 16, 4, 8400), (1,)),
         ((2, 4, 16, 2100), (2,)),
+        # every lanes-per-row bucket of the row kernel (fp16 / fp32 16-byte chunks)
+        ((9, 24), (1,)), ((3, 64), (1,)), ((5, 200), (1,)), ((3, 4000), (1,)), ((2, 2000), (1,)),
+        ((7, 512), (1,)), ((3, 1024), (1,)),
     ):
         x = (torch.randn(shape, generator=g) * 3).to(dtype)
         xd = x.to(gpu)

@@ -60,65 +60,88 @@ __device__ __forceinline__ void col_offsets(const SoftmaxPlan& p, uint32_t e, in
 }
 
 // ---------------------------------------------------------------- rows
-// One wavefront per row; lane l holds chunks l, l+64, ... (KPT of them), a
-// chunk being VE elements (one 16-byte vector when VEC, else one element).
-template <typename TI, typename TO, bool VEC, int KPT, bool FAST>
+// G lanes per row (a power of two <= 64, so a wavefront holds 64/G rows); lane
+// g of a row holds chunks g, g+G, ... (KPT of them), a chunk being VE elements
+// (one 16-byte vector when VEC, else one element).  G is chosen so that KPT is
+// about 2: several loads in flight per lane and few idle lanes.  The row max
+// only stabilises the exponentials, so it is a plain max: a NaN element, a
+// +inf element (inf - inf) or an all -inf row (-inf - -inf) makes the sum and
+// so every output NaN, exactly as on CPU.  FAST (fp16 output): e = exp2(x *
+// log2e - m * log2e) as one fma; an error in the common term scales every e
+// alike and cancels in e / sum.
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, G));
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, G);
+  return v;
+}
+
+template <typename TI, typename TO, bool VEC, int G, int KPT, bool FAST, bool NT>
 __global__ __launch_bounds__(kThreads) void softmax_row_kernel(SoftmaxPlan p) {
   constexpr int VE = VEC ? 16 / (int)sizeof(TI) : 1;
+  constexpr int RPW = 64 / G;
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (row >= p.units) return;  // uniform per wave
-  int64_t xo, oo;
-  col_offsets(p, row, xo, oo);
+  const uint32_t g = lane % G;
+  const uint32_t row = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * RPW + lane / G;
+  const bool live = row < p.units;  // every lane still joins the group shuffles
+  int64_t xo = 0, oo = 0;
+  if (live) col_offsets(p, row, xo, oo);
   const TI* xr = static_cast<const TI*>(p.x) + xo;
   TO* orow = static_cast<TO*>(p.out) + oo;
   const uint32_t chunks = VEC ? p.R / VE : p.R;
-  float v[KPT][VE];
+  struct alignas(VE * sizeof(TI)) WI { TI e[VE]; };
+  WI raw[KPT];
   float m = -__builtin_inff();
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    const uint32_t c = lane + 64u * k;
-    if (c < chunks) {
-      if (VEC) {
-        struct alignas(16) W { TI e[VE]; };
-        W w = *reinterpret_cast<const W*>(xr + (size_t)c * VE);
+    const uint32_t c = g + G * k;
+    if (live && c < chunks) {
+      const WI* src = reinterpret_cast<const WI*>(xr) + c;
+      if constexpr (VEC && NT) raw[k] = __builtin_bit_cast(WI, __builtin_nontemporal_load(
+                                   reinterpret_cast<const uint32_t __attribute__((ext_vector_type(4)))*>(src)));
+      else raw[k] = *src;
 #pragma unroll
-        for (int j = 0; j < VE; ++j) v[k][j] = (float)w.e[j];
-      } else {
-        v[k][0] = ldf(xr + c);
-      }
-#pragma unroll
-      for (int j = 0; j < VE; ++j) m = max_nan(m, v[k][j]);
+      for (int j = 0; j < VE; ++j) m = fmaxf(m, (float)raw[k].e[j]);
     }
   }
-  m = wave_max_nan(m);
+  m = group_max<G>(m);
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float ml = m * kLog2e;
+  float e[KPT][VE];
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    const uint32_t c = lane + 64u * k;
-    if (c < chunks) {
+    const uint32_t c = g + G * k;
+    if (live && c < chunks) {
 #pragma unroll
       for (int j = 0; j < VE; ++j) {
-        v[k][j] = expo<FAST>(v[k][j] - m);
-        s += v[k][j];
+        const float x = (float)raw[k].e[j];
+        e[k][j] = FAST ? __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -ml)) : expf(x - m);
+        s += e[k][j];
       }
     }
   }
-  s = wave_sum(s);
+  s = group_sum<G>(s);
   const float inv = 1.0f / s;
+  struct alignas(VE * sizeof(TO)) WO { TO e[VE]; };
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    const uint32_t c = lane + 64u * k;
-    if (c < chunks) {
-      if (VEC) {
-        struct alignas(16) W { TO e[VE]; };
-        W w;
+    const uint32_t c = g + G * k;
+    if (live && c < chunks) {
+      WO w;
 #pragma unroll
-        for (int j = 0; j < VE; ++j) w.e[j] = (TO)(v[k][j] * inv);
-        *reinterpret_cast<W*>(orow + (size_t)c * VE) = w;
-      } else {
-        stf(orow + c, v[k][0] * inv);
-      }
+      for (int j = 0; j < VE; ++j) w.e[j] = (TO)(e[k][j] * inv);
+      WO* dst = reinterpret_cast<WO*>(orow) + c;
+      if constexpr (VEC && NT && sizeof(WO) == 16) __builtin_nontemporal_store(
+          __builtin_bit_cast(uint32_t __attribute__((ext_vector_type(4))), w),
+          reinterpret_cast<uint32_t __attribute__((ext_vector_type(4)))*>(dst));
+      else *dst = w;
     }
   }
 }
@@ -326,6 +349,28 @@ void column_space(const thin_desc* x, const thin_desc* out, int dim, SoftmaxPlan
   }
 }
 
+// Streaming (non-temporal) loads and stores for launches moving at least this
+// many bytes; smaller ones stay cached for their producer and consumer.
+constexpr int64_t kStreamingBytes = (int64_t)16 << 20;
+
+// Lanes per row G and chunks per lane KPT for a row of `chunks` (<= 512).
+template <typename TI, typename TO, bool VEC, bool FAST, bool NT>
+void launch_rows(const SoftmaxPlan& p, int64_t chunks, uint64_t rows, hipStream_t stream) {
+  auto grid = [&](int g) { return (uint32_t)((rows + (uint64_t)kWaves * (64 / g) - 1) / ((uint64_t)kWaves * (64 / g))); };
+#define THIN_ROWG(G, K) hipLaunchKernelGGL((softmax_row_kernel<TI, TO, VEC, G, K, FAST, NT>), dim3(grid(G)), \
+                                           dim3(kThreads), 0, stream, p)
+  if (chunks <= 2) THIN_ROWG(1, 2);
+  else if (chunks <= 4) THIN_ROWG(2, 2);
+  else if (chunks <= 8) THIN_ROWG(4, 2);
+  else if (chunks <= 16) THIN_ROWG(8, 2);
+  else if (chunks <= 32) THIN_ROWG(16, 2);
+  else if (chunks <= 64) THIN_ROWG(32, 2);
+  else if (chunks <= 128) THIN_ROWG(64, 2);
+  else if (chunks <= 256) THIN_ROWG(64, 4);
+  else THIN_ROWG(64, 8);
+#undef THIN_ROWG
+}
+
 template <typename TI, typename TO, bool FAST>
 thin_status launch_softmax(const thin_desc* x, int dim, const thin_desc* out, hipStream_t stream) {
   SoftmaxPlan p;
@@ -355,23 +400,16 @@ thin_status launch_softmax(const thin_desc* x, int dim, const thin_desc* out, hi
     bool vec = R % VE == 0 && aligned(x->data, 16) && aligned(out->data, 16);
     for (int i = 0; vec && i < p.nd; ++i)
       vec = (p.xs[i] * (int64_t)sizeof(TI)) % 16 == 0 && (p.os[i] * (int64_t)sizeof(TO)) % 16 == 0;
-    const uint32_t grid = (uint32_t)((cols + kWaves - 1) / kWaves);
-    if (vec) {
-      const int64_t chunks = R / VE;
-#define THIN_ROWK(K) hipLaunchKernelGGL((softmax_row_kernel<TI, TO, true, K, FAST>), dim3(grid), dim3(kThreads), 0, stream, p)
-      if (chunks <= 64) THIN_ROWK(1);
-      else if (chunks <= 128) THIN_ROWK(2);
-      else if (chunks <= 256) THIN_ROWK(4);
-      else if (chunks <= 512) THIN_ROWK(8);
-      else hipLaunchKernelGGL((softmax_row_stream_kernel<TI, TO, FAST>), dim3((uint32_t)cols), dim3(kThreads), 0, stream, p);
-#undef THIN_ROWK
+    const int64_t chunks = vec ? R / VE : R;
+    const bool nt = vec && (int64_t)cols * R * (int64_t)(sizeof(TI) + sizeof(TO)) >= kStreamingBytes;
+    if (chunks > 512) {
+      hipLaunchKernelGGL((softmax_row_stream_kernel<TI, TO, FAST>), dim3((uint32_t)cols), dim3(kThreads), 0, stream,
+                         p);
+    } else if (vec) {
+      if (nt) launch_rows<TI, TO, true, FAST, true>(p, chunks, cols, stream);
+      else launch_rows<TI, TO, true, FAST, false>(p, chunks, cols, stream);
     } else {
-#define THIN_ROWS(K) hipLaunchKernelGGL((softmax_row_kernel<TI, TO, false, K, FAST>), dim3(grid), dim3(kThreads), 0, stream, p)
-      if (R <= 64) THIN_ROWS(1);
-      else if (R <= 256) THIN_ROWS(4);
-      else if (R <= 1024) THIN_ROWS(16);
-      else hipLaunchKernelGGL((softmax_row_stream_kernel<TI, TO, FAST>), dim3((uint32_t)cols), dim3(kThreads), 0, stream, p);
-#undef THIN_ROWS
+      launch_rows<TI, TO, false, FAST, false>(p, chunks, cols, stream);
     }
     THIN_LAUNCH_CHECK("softmax_row");
     return THIN_OK;
