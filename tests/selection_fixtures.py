@@ -54,6 +54,8 @@ def fixtures(full=True):
         yield f"prefix-boundary-{k}", tied, k, False, "transposed", False
     for nc in (1, 15, 16, 17, 31, 80, 257):
         yield f"class-block-{nc}", predictions(2, 144, nc, seed=1000 + nc), 129, False, "transposed", False
+    for agnostic in (False, True):  # more anchors than one block holds in registers
+        yield f"large-anchors-{agnostic}", predictions(1, 40000, 2, seed=41), 300, agnostic, "transposed", False
     if full:
         patterns = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16)
         x = torch.cat((torch.zeros(1, 128, 4).half(), patterns.reshape(1, 128, 512)), -1)

@@ -56,26 +56,51 @@ struct Layout {
 
 // ---------------------------------------------------------------- stage 1
 // bits1[b,a], cls1[b,a]: the first class with the smallest key.
-__global__ __launch_bounds__(kThreads) void class_max_kernel(Layout L, int64_t batches, int64_t anchors,
-                                                              int64_t classes, uint16_t* bits1, int32_t* cls1,
-                                                              uint16_t* trace_max) {
-  const int64_t total = batches * anchors;
-  for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t < total; t += (int64_t)gridDim.x * kThreads) {
+// Wide form: a block covers 64 consecutive anchors (one per lane, so a wave
+// reads 128 contiguous bytes per class in the production [B,4+nc,A] layout)
+// and CG class groups (one per wave; group g scans classes g, g+CG, ...).  Each
+// group keeps its first minimal key; merging the groups by (key, class) keeps
+// the first class with the minimal key overall.
+template <int CG>
+__global__ __launch_bounds__(64 * CG) void class_max_wide_kernel(Layout L, int64_t batches, int64_t anchors,
+                                                                  int64_t classes, uint16_t* bits1, int32_t* cls1,
+                                                                  uint16_t* trace_max) {
+  __shared__ uint32_t g_key[CG][64], g_bits[CG][64], g_cls[CG][64];
+  const uint32_t lane = threadIdx.x & 63u, grp = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = t < batches * anchors;
+  uint32_t bk = 0x10000u, bb = 0u, bc = 0xffffffffu;
+  if (live) {
     const int64_t b = t / anchors, a = t - b * anchors;
     const uint16_t* row = L.x + b * L.sb + a * L.sa + 4 * L.sc;
-    uint32_t best = 0x10000u, best_bits = 0, best_cls = 0;
-    for (int64_t c = 0; c < classes; ++c) {
+#pragma unroll 4
+    for (int64_t c = grp; c < classes; c += CG) {
       const uint32_t bits = row[c * L.sc];
       const uint32_t k = score_key(bits);
-      if (k < best) {
-        best = k;
-        best_bits = bits;
-        best_cls = (uint32_t)c;
+      if (k < bk) {
+        bk = k;
+        bb = bits;
+        bc = (uint32_t)c;
       }
     }
-    bits1[t] = (uint16_t)best_bits;
-    cls1[t] = (int32_t)best_cls;
-    if (trace_max) trace_max[t] = (uint16_t)best_bits;
+  }
+  g_key[grp][lane] = bk;
+  g_bits[grp][lane] = bb;
+  g_cls[grp][lane] = bc;
+  __syncthreads();
+  if (grp == 0 && live) {
+#pragma unroll
+    for (int g = 1; g < CG; ++g) {
+      const uint32_t k = g_key[g][lane], c = g_cls[g][lane];
+      if (k < bk || (k == bk && c < bc)) {
+        bk = k;
+        bb = g_bits[g][lane];
+        bc = c;
+      }
+    }
+    bits1[t] = (uint16_t)bb;
+    cls1[t] = (int32_t)bc;
+    if (trace_max) trace_max[t] = (uint16_t)bb;
   }
 }
 
@@ -179,6 +204,265 @@ __global__ __launch_bounds__(kSelThreads) void topk_block_kernel(TopkPlan p) {
     }
   }
   for (uint32_t r = tid; r < K; r += kSelThreads) p.sel[(size_t)b * K + r] = (int32_t)(uint32_t)recs[r];
+}
+
+// ---------------------------------------------------------------- register top-K
+// One 1024-thread block per batch for up to 32768 candidates.  The candidate
+// bits are staged in LDS with coalesced 16-byte loads (they also serve the
+// packing step), then thread t takes candidates [t*KPT, t*KPT + KPT) into
+// registers, so thread order is index order.  Radix select: per-wave LDS histograms of the high and
+// then the low key byte, summed and scanned by 256 threads, give the threshold
+// key T and how many T-keyed candidates to keep; a block-wide exclusive scan of
+// per-thread T counts ranks the T-keyed candidates in index order (lowest index
+// kept).  The K selected records (key << 16 | index, unique) are ordered by
+// rank counting (K <= 512) or an LDS bitonic sort.  Modes: 0 writes the
+// selected indices; 1 (class-agnostic anchors) and 2 (per-class pairs, whose
+// scores a wide gather kernel collected) also pack the output rows and the
+// trace stages.
+constexpr uint32_t kRegThreads = 1024;
+constexpr uint32_t kRegWaves = kRegThreads / 64;
+constexpr uint32_t kRegMaxN = 32768;
+constexpr uint32_t kRegMaxK = 8192;
+constexpr uint32_t kRankSortMax = 512;
+
+struct RegTopkPlan {
+  const uint16_t* bits;   // candidate bits [B, n]
+  Layout L;               // boxes for packing
+  const int32_t* stage1;  // mode 2: first-stage anchors [B, K]
+  uint32_t n, K;          // candidates and selections per batch
+  FastDiv nc;             // classes (mode 2 pair index = rank * nc + class)
+  int64_t anchors;        // row pitch of bits1 / cls1 (mode 1)
+  int32_t* sel;           // mode 0: [B, K] selected candidate indices
+  const int32_t* cls1;    // mode 1: class-max labels [B, A]
+  uint32_t* out;          // modes 1, 2: [B, K, 6] fp32 bits
+  thin_select_trace tr;
+};
+
+// Exclusive block-wide prefix sum of v; `total` receives the block sum.
+__device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* wave_tot, uint32_t& total) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o);
+    if (lane >= (uint32_t)o) x += y;
+  }
+  if (lane == 63u) wave_tot[wave] = x;
+  __syncthreads();
+  uint32_t before = 0;
+  total = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kRegWaves; ++w) {
+    const uint32_t t = wave_tot[w];
+    before += w < wave ? t : 0u;
+    total += t;
+  }
+  __syncthreads();
+  return before + x - v;
+}
+
+// Sums the per-wave histograms and finds the bin q with
+// base + count(< q) < need <= base + count(<= q); writes q and base + count(< q).
+__device__ __forceinline__ void pick_bin(uint32_t (*hist)[256], uint32_t base, uint32_t need, uint32_t* wave_tot,
+                                         uint32_t* result) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t h = 0;
+  if (tid < 256) {
+#pragma unroll
+    for (uint32_t w = 0; w < kRegWaves; ++w) h += hist[w][tid];
+  }
+  uint32_t total;
+  const uint32_t excl = block_exclusive_sum(tid < 256 ? h : 0u, wave_tot, total);
+  if (tid < 256 && base + excl < need && need <= base + excl + h) {
+    result[0] = tid;
+    result[1] = base + excl;
+  }
+  __syncthreads();
+}
+
+// Output row r of batch b for selected candidate idx; `staged` holds the
+// batch's candidate bits (the selected score's bits are staged[idx]).
+template <int MODE>
+__device__ __forceinline__ void pack_row(const RegTopkPlan& p, const uint16_t* staged, uint32_t b, uint32_t r,
+                                         uint32_t idx) {
+  int64_t a, label;
+  const uint32_t sbits = staged[idx];
+  if (MODE == 1) {
+    a = idx;
+    label = p.cls1[(int64_t)b * p.anchors + a];
+  } else {
+    const uint32_t rank1 = p.nc.div(idx);
+    label = idx - rank1 * p.nc.d;
+    a = p.stage1[(size_t)b * p.K + rank1];
+  }
+  const uint16_t* box = p.L.x + b * p.L.sb + a * p.L.sa;
+  const size_t t = (size_t)b * p.K + r;
+  uint32_t* o = p.out + t * 6;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) o[c] = float_bits(box[c * p.L.sc]);
+  o[4] = float_bits(sbits);
+  o[5] = __float_as_uint((float)label);
+  if (p.tr.stage1) static_cast<int64_t*>(p.tr.stage1)[t] = MODE == 1 ? a : (int64_t)p.stage1[t];
+  if (MODE == 2 && p.tr.stage2) static_cast<int64_t*>(p.tr.stage2)[t] = idx;
+  if (p.tr.anchors) static_cast<int64_t*>(p.tr.anchors)[t] = a;
+  if (p.tr.labels) static_cast<int64_t*>(p.tr.labels)[t] = label;
+  if (p.tr.top_values) static_cast<uint16_t*>(p.tr.top_values)[t] = (uint16_t)sbits;
+}
+
+// Histogram update for a thread's keys: the high byte (hi == 0xffffffff) or
+// the low byte of keys whose high byte is hi.  Equal bins of consecutive
+// candidates are merged first, so skewed score distributions (most class
+// maxima in one bin) cost one LDS atomic per run instead of one per key.
+template <int KPT>
+__device__ __forceinline__ void count_bins(uint32_t* hist, const uint32_t (&key)[KPT], uint32_t hi) {
+  uint32_t cur = 0xffffffffu, run = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const bool in = hi == 0xffffffffu ? key[j] <= 0xffffu : (key[j] >> 8) == hi;
+    if (!in) continue;
+    const uint32_t bin = hi == 0xffffffffu ? key[j] >> 8 : key[j] & 0xffu;
+    if (bin != cur) {
+      if (run) atomicAdd(&hist[cur], run);
+      cur = bin;
+      run = 0;
+    }
+    ++run;
+  }
+  if (run) atomicAdd(&hist[cur], run);
+}
+
+template <int MODE, int KPT>
+__global__ __launch_bounds__(kRegThreads) void topk_reg_kernel(RegTopkPlan p) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) uint16_t staged[kRegMaxN];
+  __shared__ uint32_t hist[kRegWaves][256];
+  __shared__ __attribute__((aligned(16))) uint32_t recs[kRegMaxK];
+  __shared__ uint32_t wave_tot[kRegWaves];
+  __shared__ uint32_t result[2];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
+  const uint32_t n = p.n, K = p.K;
+  const uint32_t first = tid * KPT;
+
+  // stage the batch's candidate bits in LDS (coalesced), then take this
+  // thread's KPT consecutive keys (0xffffffff past the end)
+  const uint16_t* src = p.bits + (size_t)b * n;
+  uint32_t head = 0;
+  if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+    head = n & ~7u;
+    for (uint32_t v = tid; v < head / 8; v += kRegThreads)
+      reinterpret_cast<u4*>(staged)[v] = reinterpret_cast<const u4*>(src)[v];
+  }
+  for (uint32_t i = head + tid; i < n; i += kRegThreads) staged[i] = src[i];
+  __syncthreads();
+  uint32_t key[KPT];
+#pragma unroll
+  for (int v = 0; v < KPT / 8; ++v) {
+    const u4 w = reinterpret_cast<const u4*>(staged + first)[v];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      key[v * 8 + 2 * h] = w[h] & 0xffffu;
+      key[v * 8 + 2 * h + 1] = w[h] >> 16;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) key[j] = first + j < n ? score_key(key[j]) : 0xffffffffu;
+
+  // level 1: high byte
+  for (uint32_t q = tid; q < kRegWaves * 256; q += kRegThreads) (&hist[0][0])[q] = 0;
+  __syncthreads();
+  count_bins<KPT>(hist[wave], key, 0xffffffffu);
+  __syncthreads();
+  pick_bin(hist, 0, K, wave_tot, result);
+  const uint32_t b1 = result[0], below1 = result[1];
+  // level 2: low byte inside bucket b1
+  for (uint32_t q = tid; q < kRegWaves * 256; q += kRegThreads) (&hist[0][0])[q] = 0;
+  __syncthreads();
+  count_bins<KPT>(hist[wave], key, b1);
+  __syncthreads();
+  pick_bin(hist, below1, K, wave_tot, result);
+  const uint32_t T = (b1 << 8) | result[0];
+  const uint32_t need = K - result[1];  // T-keyed candidates kept, lowest index first
+
+  // rank the T-keyed candidates in index order, then place the selected ones
+  uint32_t eq = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) eq += key[j] == T ? 1u : 0u;
+  uint32_t total;
+  uint32_t eq_before = block_exclusive_sum(eq, wave_tot, total);
+  uint32_t mine = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const bool take = key[j] < T || (key[j] == T && eq_before < need);
+    eq_before += key[j] == T ? 1u : 0u;
+    key[j] = take ? key[j] : 0xffffffffu;  // reuse: 0xffffffff = not selected
+    mine += take ? 1u : 0u;
+  }
+  uint32_t pos = block_exclusive_sum(mine, wave_tot, total);
+#pragma unroll
+  for (int j = 0; j < KPT; ++j)
+    if (key[j] != 0xffffffffu) recs[pos++] = (key[j] << 16) | (first + j);
+  __syncthreads();
+
+  if (K <= kRankSortMax) {
+    // rank counting: records are unique, so ranks are a permutation; the pad
+    // up to a multiple of 16 (0xffffffff) is above every record
+    const uint32_t K16 = (K + 15u) & ~15u;
+    if (tid >= K && tid < K16) recs[tid] = 0xffffffffu;
+    __syncthreads();
+    if (tid < K) {
+      const uint32_t rec = recs[tid];
+      uint32_t rank = 0;
+      typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+      const u4* r4 = reinterpret_cast<const u4*>(recs);
+      for (uint32_t u = 0; u < K16 / 4; u += 4) {
+        u4 q[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) q[h] = r4[u + h];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          rank += (q[h].x < rec) + (q[h].y < rec) + (q[h].z < rec) + (q[h].w < rec);
+      }
+      const uint32_t idx = rec & 0xffffu;
+      if (MODE == 0) p.sel[(size_t)b * K + rank] = (int32_t)idx;
+      else pack_row<MODE>(p, staged, b, rank, idx);
+    }
+    return;
+  }
+  uint32_t P = 1;
+  while (P < K) P <<= 1;
+  for (uint32_t i = K + tid; i < P; i += kRegThreads) recs[i] = 0xffffffffu;
+  __syncthreads();
+  for (uint32_t size = 2; size <= P; size <<= 1) {
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      for (uint32_t i = tid; i < P; i += kRegThreads) {
+        const uint32_t l = i ^ stride;
+        if (l > i) {
+          const uint32_t x = recs[i], y = recs[l];
+          const bool up = (i & size) == 0;
+          if ((x > y) == up) {
+            recs[i] = y;
+            recs[l] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (uint32_t r = tid; r < K; r += kRegThreads) {
+    const uint32_t idx = recs[r] & 0xffffu;
+    if (MODE == 0) p.sel[(size_t)b * K + r] = (int32_t)idx;
+    else pack_row<MODE>(p, staged, b, r, idx);
+  }
+}
+
+template <int MODE>
+void launch_reg_topk(const RegTopkPlan& p, int64_t B, hipStream_t stream) {
+  if (p.n <= 8u * kRegThreads)
+    hipLaunchKernelGGL((topk_reg_kernel<MODE, 8>), dim3((uint32_t)B), dim3(kRegThreads), 0, stream, p);
+  else if (p.n <= 16u * kRegThreads)
+    hipLaunchKernelGGL((topk_reg_kernel<MODE, 16>), dim3((uint32_t)B), dim3(kRegThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((topk_reg_kernel<MODE, 32>), dim3((uint32_t)B), dim3(kRegThreads), 0, stream, p);
 }
 
 // Large K: records for every candidate, padded to P (power of two) per batch.
@@ -387,16 +671,53 @@ extern "C" thin_status thin_detection_select(const thin_desc* decoded, int64_t m
 
   Layout L{static_cast<const uint16_t*>(decoded->data), decoded->strides[0], decoded->strides[1],
            decoded->strides[2]};
-  hipLaunchKernelGGL(class_max_kernel, dim3(blocks_for((uint64_t)(B * A))), dim3(kThreads), 0, stream, L, B, A, nc,
-                     bits1, cls1, static_cast<uint16_t*>(tr.class_max));
+  constexpr int kGroups = 16;
+  hipLaunchKernelGGL((class_max_wide_kernel<kGroups>), dim3((uint32_t)((B * A + 63) / 64)), dim3(64 * kGroups), 0,
+                     stream, L, B, A, nc, bits1, cls1, static_cast<uint16_t*>(tr.class_max));
   THIN_LAUNCH_CHECK("class_max");
   if (K == 0) return THIN_OK;
-  thin_status s = topk(bits1, B, A, K, stage1, recs, w.recs_pitch, stream);
-  if (s) return s;
+  RegTopkPlan rp;
+  memset(&rp, 0, sizeof rp);
+  rp.L = L;
+  rp.K = (uint32_t)K;
+  rp.nc = FastDiv::make((uint32_t)nc);
+  rp.anchors = A;
+  rp.out = static_cast<uint32_t*>(out);
+  rp.tr = tr;
+  const bool reg1 = A <= (int64_t)kRegMaxN && K <= (int64_t)kRegMaxK;
+  const bool reg2 = K * nc <= (int64_t)kRegMaxN && K <= (int64_t)kRegMaxK;
+  if (agn && reg1) {  // one launch: select anchors by their class max and pack
+    rp.bits = bits1;
+    rp.n = (uint32_t)A;
+    rp.cls1 = cls1;
+    launch_reg_topk<1>(rp, B, stream);
+    THIN_LAUNCH_CHECK("topk_pack");
+    return THIN_OK;
+  }
+  thin_status s;
+  if (reg1) {
+    rp.bits = bits1;
+    rp.n = (uint32_t)A;
+    rp.sel = stage1;
+    launch_reg_topk<0>(rp, B, stream);
+    THIN_LAUNCH_CHECK("topk_stage1");
+  } else {
+    s = topk(bits1, B, A, K, stage1, recs, w.recs_pitch, stream);
+    if (s) return s;
+  }
   if (!agn) {
     hipLaunchKernelGGL(gather_kernel, dim3(blocks_for((uint64_t)(B * K * nc))), dim3(kThreads), 0, stream, L, B, K,
                        nc, stage1, gathered, static_cast<uint16_t*>(tr.gathered));
     THIN_LAUNCH_CHECK("gather");
+    if (reg2) {  // select pairs over the gathered scores and pack
+      rp.bits = gathered;
+      rp.stage1 = stage1;
+      rp.n = (uint32_t)(K * nc);
+      rp.sel = nullptr;
+      launch_reg_topk<2>(rp, B, stream);
+      THIN_LAUNCH_CHECK("topk_stage2");
+      return THIN_OK;
+    }
     s = topk(gathered, B, K * nc, K, stage2, recs, w.recs_pitch, stream);
     if (s) return s;
   }
