@@ -231,6 +231,14 @@ def op_softmax(capi, dev, n, rotate=True):
     return (lambda st: capi.softmax(st[0], 3, out=st[1])), sets, algo
 
 
+def op_maxpool(capi, dev, n, rotate=True):
+    """SPPF max pool k5 on NC1HWC0 [n,256,20,20] (one of the three chained pools)."""
+    algo = n * 16 * 20 * 20 * 16 * 2 * 2
+    sets = rotated(lambda i: (blocked_normal(n, 256, 20, 20, 210 + i, dev),
+                              torch.empty((n, 16, 20, 20, 16), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.maxpool_nc1hwc0(st[0], 5, out=st[1])), sets, algo
+
+
 def op_select(capi, dev, layout, rotate=False):
     """C5 NMS-free top-300 of [1,8400,84] (latency-bound: report us)."""
     from tests.selection_fixtures import c5_selection_input  # input generator, shared with the tests
@@ -263,6 +271,7 @@ def op_rows(capi, dev):
         rows.append(("dfl_expect_64x8400", "C4", n, lambda r, n=n: op_dfl(capi, dev, n, r)))
         rows.append(("sigmoid_80x8400", "C4", n, lambda r, n=n: op_sigmoid(capi, dev, n, r)))
         rows.append(("softmax_4x400x400", "C5", n, lambda r, n=n: op_softmax(capi, dev, n, r)))
+        rows.append(("maxpool_k5_256x20x20", "SPPF", n, lambda r, n=n: op_maxpool(capi, dev, n, r)))
     for layout in ("contiguous", "transposed"):
         rows.append((f"detection_select_{layout}", "C5", 1, lambda r, l=layout: op_select(capi, dev, l)))
     return rows

@@ -160,6 +160,25 @@ thin_status thin_pack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_
  * Replaces thin_blocked::unpack (layout_blocked.h:57-69); any N. */
 thin_status thin_unpack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_t stream);
 
+/* Stride-1 max pool, odd kernel k in [1, 15], "same" padding (taps outside
+ * the plane skipped): out[n,c1,y,x,:] = max over the k x k window of x.  The
+ * first maximum in row-major window order is kept (PyTorch CPU's choice for
+ * +0/-0 ties); a NaN in the window gives NaN.  fp16 NC1HWC0, any N, N/C1/H
+ * strides free, pixels 16-byte aligned.  Replaces blocked_flow::maxpool and
+ * maxpool_tiles (flow_ops.cpp:82-127,208-231; SPPF k5). */
+thin_status thin_maxpool_nc1hwc0(const thin_desc* x, int32_t kernel, const thin_desc* out, hipStream_t stream);
+
+/* The same pool over NCHW fp16/fp32, any strides.  Replaces thin::maxpool2d
+ * (backend.cpp:245-266; maxpool.cpp:1-60, k5 s1 p2) and serves aten
+ * max_pool2d_with_indices (aten_adapter.cpp:61-80). */
+thin_status thin_maxpool2d_nchw(const thin_desc* x, int32_t kernel, const thin_desc* out, hipStream_t stream);
+
+/* out[...] = value (float dtypes) or ivalue (integer dtypes), any strides.
+ * Replaces the device side of aten fill_.Scalar / zero_ (decode.cpp:29-34)
+ * and the zero placeholder indices of max_pool2d_with_indices
+ * (aten_adapter.cpp:71-78); a kernel, so safe inside graph capture. */
+thin_status thin_fill(const thin_desc* out, double value, int64_t ivalue, hipStream_t stream);
+
 /* ------------------------------------------------------------------ */
 /* Reductions                                                          */
 /* ------------------------------------------------------------------ */

@@ -11,15 +11,21 @@ Every function moves bits only, so parity is bit-exact (NaN payloads included).
   pack_blocked(x)            -- NCHW -> NC1HWC0, channels >= C zero
                                 (conv_flow.cpp:406-443; layout_blocked.h:2-55)
   unpack_blocked(y, c)       -- inverse, first c channels (layout_blocked.h:57-69)
+  maxpool_nchw(x, k)         -- stride-1 k x k max pool, padding k//2, via PyTorch CPU on
+                                fp32 (verify_flow_ops.py:31-33; backend.cpp:245-266)
+  maxpool_blocked(x, k)      -- the same pool on NC1HWC0 (flow_ops.cpp:82-127,208-231)
 
 Pinning (tests/test_oracle_movement.py): cat against torch.cat; the upsamples
 against torch's F.interpolate(mode="nearest") and brute-force loops; pack and
-unpack against brute-force index loops and the pack -> unpack round trip.
+unpack against brute-force index loops and the pack -> unpack round trip; the
+max pools against a brute-force window loop (first maximum in row-major order,
+NaN if the window holds one) with +0/-0 ties, infinities and NaNs.
 """
 from __future__ import annotations
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 _INT = {1: np.uint8, 2: np.int16, 4: np.int32, 8: np.int64}
 _TINT = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}
@@ -73,3 +79,17 @@ def unpack_blocked(y: torch.Tensor, channels: int | None = None) -> torch.Tensor
     n, c1, h, w, c0 = b.shape
     c = c1 * c0 if channels is None else channels
     return _from_bits(b.transpose(0, 1, 4, 2, 3).reshape(n, c1 * c0, h, w)[:, :c], y)
+
+
+def maxpool_nchw(x: torch.Tensor, kernel: int) -> torch.Tensor:
+    """F.max_pool2d on fp32, stride 1, padding kernel // 2, cast back: max only
+    selects existing values, so the fp32 detour is exact (verify_flow_ops.py:31-33)."""
+    return F.max_pool2d(x.float(), kernel, stride=1, padding=kernel // 2).to(x.dtype)
+
+
+def maxpool_blocked(x: torch.Tensor, kernel: int) -> torch.Tensor:
+    """maxpool_nchw on the NCHW view of an NC1HWC0 tensor, repacked."""
+    n, c1, h, w, c0 = x.shape
+    nchw = x.permute(0, 1, 4, 2, 3).reshape(n, c1 * c0, h, w)
+    y = maxpool_nchw(nchw, kernel)
+    return y.reshape(n, c1, c0, h, w).permute(0, 1, 3, 4, 2).contiguous()

@@ -120,8 +120,15 @@ def test_aten_routes_and_rejects(npu):
         assert torch.full((2, 3), 2.0, device="npu").cpu().eq(2).all()
         assert torch.zeros(4, device="npu").cpu().eq(0).all()
         assert torch.tensor(1.5).to("npu").item() == 1.5
+        # aten max_pool2d k5/s1/p2 (aten_adapter.cpp:61-80): values, zero placeholder indices
+        assert bits_equal(F.max_pool2d(an, 5, 1, 2).cpu(), F.max_pool2d(a, 5, 1, 2))
+        values, indices = torch.ops.aten.max_pool2d_with_indices(a.half().to(npu), [5, 5], [1, 1], [2, 2])
+        assert bits_equal(values.cpu(), F.max_pool2d(a.half().float(), 5, 1, 2).half())
+        assert indices.dtype == torch.int64 and not indices.cpu().any()
+        assert bits_equal(torch.ops.thin_backend.maxpool2d(an).cpu(), F.max_pool2d(a, 5, 1, 2))
         for name, op in (("conv", lambda: F.conv2d(an, torch.randn(3, 7, 3, 3).to(npu))),
-                         ("pool", lambda: F.max_pool2d(an, 5, 1, 2)),
+                         ("pool-k3", lambda: F.max_pool2d(an, 3, 1, 1)),
+                         ("pool-s2", lambda: F.max_pool2d(an, 5, 2, 2)),
                          ("nearest-3x", lambda: F.interpolate(an, scale_factor=3, mode="nearest"))):
             with pytest.raises(RuntimeError, match="thin aten"):
                 op()
@@ -277,8 +284,11 @@ def test_flow_ops(npu):
         y = torch.ops.thin_blocked.pack(x.to(npu))
         assert bits_equal(y.cpu(), mv.pack_blocked(x))
         assert bits_equal(torch.ops.thin_blocked.unpack(y).cpu(), x)
-        with pytest.raises(RuntimeError, match="not provided"):
-            torch.ops.thin_native_flow.maxpool(y, 5)
+        xm = normal16((2, 64, 20, 20), 5)
+        ym = torch.ops.thin_blocked.pack(xm.to(npu))
+        assert bits_equal(torch.ops.thin_native_flow.maxpool(ym, 5).cpu(), mv.maxpool_blocked(mv.pack_blocked(xm), 5))
+        with pytest.raises(RuntimeError, match="odd"):
+            torch.ops.thin_native_flow.maxpool(ym, 4)
 
 
 def test_fused_ops(npu):

@@ -171,3 +171,83 @@ def test_movement_errors(gpu):
     with pytest.raises(capi.ThinError):
         capi.upsample_cat_nc1hwc0([torch.zeros(1, 1, 2, 2, 16, device=gpu, dtype=torch.float16)], [False],
                                   out=torch.zeros(1, 1, 4, 4, 16, device=gpu, dtype=torch.float16))
+
+
+MAXPOOL_SHAPES = [(256, 20, 20, 5), (128, 40, 40, 5), (512, 20, 20, 5), (32, 13, 17, 3), (16, 7, 9, 7),
+                  (48, 1, 31, 5)]
+
+
+def pool_specials(x):
+    """+0/-0 ties in both orders, infinities and NaNs written into x (fp16)."""
+    x = x.clone()
+    flat = x.view(-1)
+    n = flat.numel()
+    g = gen(77)
+    for value, count in ((0.0, n // 20), (-0.0, n // 20), (float("inf"), 3), (float("-inf"), 5), (float("nan"), 4)):
+        flat[torch.randint(0, n, (count,), generator=g)] = value
+    return x
+
+
+def check_pool(got, want, what):
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got), nan), f"{what}: NaN mask"
+    assert bits_equal(got[~nan], want[~nan]), f"{what}: bits"
+
+
+@pytest.mark.parametrize("n", [1, 3])
+def test_maxpool_nc1hwc0(gpu, n):
+    """verify_flow_ops.py:55-67 shapes (SPPF k5 and odd windows), any N."""
+    from thintnpu_amd import capi
+    for c, h, w, k in MAXPOOL_SHAPES:
+        x = to_blocked(normal16((n, c, h, w), c + h + k))
+        check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"{c}x{h}x{w} k{k}")
+    x = pool_specials(to_blocked(normal16((n, 32, 9, 11), 5)))
+    for k in (1, 3, 5, 7, 9, 11, 13, 15):
+        check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"specials k{k}")
+
+
+def test_maxpool_views(gpu):
+    from thintnpu_amd import capi
+    x = to_blocked(normal16((2, 64, 12, 10), 8))
+    xd = x.to(gpu)
+    got = capi.maxpool_nc1hwc0(xd[:, 1:3], 5).cpu()
+    check_pool(got, mv.maxpool_blocked(x[:, 1:3].contiguous(), 5), "channel-block slice")
+    parent = random_bits16((2, 6, 12, 10, 16), 9)
+    pd = parent.to(gpu)
+    capi.maxpool_nc1hwc0(xd[:, :2], 3, out=pd[:, 4:6])
+    got = pd.cpu()
+    check_pool(got[:, 4:6], mv.maxpool_blocked(x[:, :2].contiguous(), 3), "narrowed output")
+    assert bits_equal(got[:, :4], parent[:, :4])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_maxpool2d_nchw(gpu, dtype):
+    """thin_backend.maxpool2d (backend.cpp:245-266) semantics, any odd k, any strides."""
+    from thintnpu_amd import capi
+    x = pool_specials(normal16((2, 5, 13, 17), 3)).to(dtype)
+    for k in (1, 3, 5, 7, 15):
+        check_pool(capi.maxpool2d_nchw(x.to(gpu), k).cpu(), mv.maxpool_nchw(x, k), f"nchw k{k}")
+    t = x.transpose(2, 3)
+    check_pool(capi.maxpool2d_nchw(x.to(gpu).transpose(2, 3), 5).cpu(), mv.maxpool_nchw(t.contiguous(), 5),
+               "transposed")
+    with pytest.raises(capi.ThinError, match="odd integer"):
+        capi.maxpool2d_nchw(x.to(gpu), 4)
+
+
+def test_fill(gpu):
+    from thintnpu_amd import capi
+    for dtype, value in ((torch.float16, 1.5), (torch.float32, -2.25), (torch.float64, 1e300), (torch.bfloat16, 3.0),
+                         (torch.int64, 2 ** 60 + 1), (torch.int32, -7), (torch.int16, 300), (torch.uint8, 200),
+                         (torch.bool, 1), (torch.float16, float("nan")), (torch.float32, float("-inf"))):
+        t = torch.zeros((3, 37, 5), dtype=dtype, device=gpu)
+        capi.fill(t, value)
+        want = torch.full((3, 37, 5), value, dtype=dtype)
+        assert torch.equal(t.cpu(), want) or (dtype.is_floating_point and torch.isnan(want).all() and
+                                              torch.isnan(t.cpu()).all()), (dtype, value)
+        parent = torch.zeros((3, 37, 9), dtype=dtype, device=gpu)
+        capi.fill(parent[:, ::2, 1:6], value)
+        ref = torch.zeros((3, 37, 9), dtype=dtype)
+        ref[:, ::2, 1:6] = want[:, :19]
+        got = parent.cpu()
+        assert torch.equal(torch.isnan(got.float()), torch.isnan(ref.float())) if dtype.is_floating_point else True
+        assert torch.equal(got.nan_to_num(), ref.nan_to_num()) if dtype.is_floating_point else torch.equal(got, ref)

@@ -1,12 +1,15 @@
 """Pins the data-movement oracle (CPU only)."""
 import itertools
 
+import numpy as np
+import pytest
+
 import torch
 import torch.nn.functional as F
 
 from oracle import movement as mv
 from oracle.numerics import bits_equal
-from tests.helpers import random_bits16
+from tests.helpers import random_bits16, to_blocked
 
 
 def test_cat_matches_torch_cat_bits():
@@ -63,3 +66,46 @@ def test_upsample_cat_composition():
     assert got.shape == (2, 3, 6, 8, 16)
     assert bits_equal(got[:, :2], mv.upsample2x_blocked(a))
     assert bits_equal(got[:, 2:], b)
+
+
+def brute_maxpool(x: np.ndarray, k: int) -> np.ndarray:
+    """Window max by hand: first strictly greater value in row-major window
+    order, NaN if the window holds a NaN."""
+    n, c, h, w = x.shape
+    r = k // 2
+    out = np.empty_like(x)
+    for i in np.ndindex(n, c, h, w):
+        b, ch, yy, xx = i
+        best, nan = None, False
+        for dy in range(-r, r + 1):
+            for dx in range(-r, r + 1):
+                sy, sx = yy + dy, xx + dx
+                if 0 <= sy < h and 0 <= sx < w:
+                    v = x[b, ch, sy, sx]
+                    if np.isnan(v):
+                        nan = True
+                    elif best is None or v > best:
+                        best = v
+        out[i] = np.float16("nan") if nan else best
+    return out
+
+
+@pytest.mark.parametrize("k", [1, 3, 5, 7])
+def test_maxpool_against_brute_force(k):
+    g = torch.Generator().manual_seed(k)
+    x = torch.randn(2, 3, 6, 7, generator=g).half()
+    # ties between +0 and -0 in both orders, infinities, a NaN
+    x[0, 0, 2, 2], x[0, 0, 2, 3] = -0.0, 0.0
+    x[0, 0, 0:6, 0:7] = torch.where(x[0, 0] > 0, -x[0, 0], x[0, 0])  # plane 0 all <= 0
+    x[0, 0, 3, 1], x[0, 0, 1, 4] = 0.0, -0.0
+    x[0, 1, 1, 1] = float("inf")
+    x[1, 2, 4, 4] = float("-inf")
+    x[1, 1, 2, 5] = float("nan")
+    got = mv.maxpool_nchw(x, k)
+    want = torch.from_numpy(brute_maxpool(x.numpy(), k))
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got), nan)
+    assert bits_equal(got[~nan], want[~nan])
+    blocked = to_blocked(torch.cat((x, x.flip(1), x, x.flip(2), x, x), 1)[:, :16])
+    assert bits_equal(mv.maxpool_blocked(blocked, k),
+                      to_blocked(mv.maxpool_nchw(torch.cat((x, x.flip(1), x, x.flip(2), x, x), 1)[:, :16], k)))

@@ -26,6 +26,7 @@ SIGMOID, SILU = 0, 1
 _DTYPES = {
     torch.float16: F16, torch.float32: F32, torch.int64: I64, torch.int32: I32,
     torch.int16: I16, torch.uint8: U8, torch.float64: F64, torch.bfloat16: BF16,
+    torch.int8: U8, torch.bool: U8,  # byte-sized: moved and filled as raw bytes
 }
 STATUS = {0: "THIN_OK", 1: "THIN_ERR_INVALID", 2: "THIN_ERR_UNSUPPORTED", 3: "THIN_ERR_HIP",
           4: "THIN_ERR_WORKSPACE"}
@@ -80,6 +81,9 @@ def lib() -> ctypes.CDLL:
             "thin_unpack_nc1hwc0": [P, P, vp],
             "thin_softmax": [P, i32, P, vp],
             "thin_dfl_expect": [P, P, vp],
+            "thin_maxpool_nc1hwc0": [P, i32, P, vp],
+            "thin_maxpool2d_nchw": [P, i32, P, vp],
+            "thin_fill": [P, f64, i64, vp],
             "thin_detection_select": [P, i64, i32, vp, vp, ctypes.c_size_t,
                                       ctypes.POINTER(ThinSelectTrace), vp],
         }
@@ -241,6 +245,27 @@ def unpack_nc1hwc0(x, channels: int | None = None, out=None, stream=None):
     out = torch.empty((n, c, h, w), dtype=x.dtype, device=x.device) if out is None else out
     _call("thin_unpack_nc1hwc0", _ref(desc(x)), _ref(desc(out)), _stream(stream))
     return out
+
+
+def maxpool_nc1hwc0(x, kernel: int, out=None, stream=None):
+    """Stride-1 k x k max pool with padding k//2 on NC1HWC0 fp16."""
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
+    _call("thin_maxpool_nc1hwc0", _ref(desc(x)), kernel, _ref(desc(out)), _stream(stream))
+    return out
+
+
+def maxpool2d_nchw(x, kernel: int, out=None, stream=None):
+    """Stride-1 k x k max pool with padding k//2 on NCHW fp16/fp32."""
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
+    _call("thin_maxpool2d_nchw", _ref(desc(x)), kernel, _ref(desc(out)), _stream(stream))
+    return out
+
+
+def fill(t, value, stream=None):
+    """t[...] = value in place (any strides)."""
+    ival = int(value) if not t.is_floating_point() else 0
+    _call("thin_fill", _ref(desc(t)), float(value), ival, _stream(stream))
+    return t
 
 
 def softmax(x, dim: int, half_to_float: bool = False, out=None, stream=None):

@@ -688,6 +688,61 @@ thin_status dispatch_float(const thin_desc* out, const thin_desc* const* ins, fl
 
 }  // namespace
 
+// ------------------------------------------------------------ fill
+// out[...] = one element bit pattern.  Dense outputs take 16-byte stores of the
+// replicated pattern; any other layout walks the coalesced dims.
+__global__ __launch_bounds__(kThreads) void fill_dense_kernel(u32x4* out, uint64_t words, u32x4 pattern) {
+  for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < words; i += (uint64_t)gridDim.x * kThreads)
+    out[i] = pattern;
+}
+
+struct FillPlan {
+  char* out;
+  int32_t nd;
+  int64_t size[kMaxDims];    // innermost first
+  int64_t stride[kMaxDims];  // elements
+  uint64_t total;
+  uint64_t bits;
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void fill_strided_kernel(FillPlan p) {
+  const T v = __builtin_bit_cast(T, (typename std::conditional<sizeof(T) == 8, uint64_t,
+                                     typename std::conditional<sizeof(T) == 4, uint32_t,
+                                     typename std::conditional<sizeof(T) == 2, uint16_t, uint8_t>::type>::type>::type)p.bits);
+  for (uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x; e < p.total; e += (uint64_t)gridDim.x * kThreads) {
+    uint64_t rest = e;
+    int64_t off = 0;
+    for (int d = 0; d < p.nd; ++d) {
+      const uint64_t q = rest / (uint64_t)p.size[d];
+      off += (int64_t)(rest - q * (uint64_t)p.size[d]) * p.stride[d];
+      rest = q;
+    }
+    reinterpret_cast<T*>(p.out)[off] = v;
+  }
+}
+
+// Element bits of `value` (float dtypes) or `ivalue` (integer dtypes).
+uint64_t fill_bits(int32_t dtype, double value, int64_t ivalue) {
+  switch (dtype) {
+    case THIN_F16: return __builtin_bit_cast(uint16_t, (_Float16)(float)value);
+    case THIN_BF16: {
+      const float f = (float)value;
+      uint32_t u = __builtin_bit_cast(uint32_t, f);
+      if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+      u += 0x7fffu + ((u >> 16) & 1u);                                               // round to nearest even
+      return (uint16_t)(u >> 16);
+    }
+    case THIN_F32: return __builtin_bit_cast(uint32_t, (float)value);
+    case THIN_F64: return __builtin_bit_cast(uint64_t, value);
+    case THIN_I64: return (uint64_t)ivalue;
+    case THIN_I32: return (uint32_t)(int32_t)ivalue;
+    case THIN_I16: return (uint16_t)(int16_t)ivalue;
+    case THIN_U8: return (uint8_t)ivalue;
+  }
+  return 0;
+}
+
 // Raw bit copy used by the copy/cat/materialize paths.
 thin_status copy_bits(const thin_desc* src, const thin_desc* dst, hipStream_t stream) {
   const thin_desc* ins[1] = {src};
@@ -806,4 +861,49 @@ extern "C" thin_status thin_copy(const thin_desc* src, const thin_desc* dst, hip
   THIN_REQUIRE(dtype_size(src->dtype) == dtype_size(dst->dtype) && src->dtype == dst->dtype,
                THIN_ERR_INVALID, "copy requires matching dtypes");
   return copy_bits(src, dst, stream);
+}
+
+extern "C" thin_status thin_fill(const thin_desc* out, double value, int64_t ivalue, hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(desc_valid(out), THIN_ERR_INVALID, "fill: invalid descriptor");
+  const int64_t total = numel(out);
+  if (total == 0) return THIN_OK;
+  const int esz = dtype_size(out->dtype);
+  const uint64_t bits = fill_bits(out->dtype, value, ivalue);
+  const thin_desc* ops[1] = {out};
+  Coalesced c = coalesce(ops, 1);
+  const bool dense = c.nd == 1 && c.stride[0][0] == 1;
+  if (dense && reinterpret_cast<uintptr_t>(out->data) % 16 == 0 && (total * esz) % 16 == 0) {
+    uint32_t lanes[4];
+    for (int w = 0; w < 4; ++w) {
+      uint32_t word = 0;
+      for (int b = 0; b < 4; ++b) word |= (uint32_t)((bits >> (8 * ((w * 4 + b) % esz))) & 0xffu) << (8 * b);
+      lanes[w] = word;
+    }
+    const u32x4 pattern = {lanes[0], lanes[1], lanes[2], lanes[3]};
+    const uint64_t words = (uint64_t)total * esz / 16;
+    hipLaunchKernelGGL(fill_dense_kernel, dim3(grid_for(words, kThreads, 1, 65536u)), dim3(kThreads), 0, stream,
+                       static_cast<u32x4*>(out->data), words, pattern);
+    THIN_LAUNCH_CHECK("fill");
+    return THIN_OK;
+  }
+  FillPlan p;
+  memset(&p, 0, sizeof p);
+  p.out = static_cast<char*>(out->data);
+  p.nd = c.nd;
+  for (int i = 0; i < c.nd; ++i) {
+    p.size[i] = c.size[c.nd - 1 - i];
+    p.stride[i] = c.stride[0][c.nd - 1 - i];
+  }
+  p.total = (uint64_t)total;
+  p.bits = bits;
+  const uint32_t grid = grid_for((uint64_t)total, kThreads, 1, 65536u);
+  switch (esz) {
+    case 1: hipLaunchKernelGGL(fill_strided_kernel<uint8_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(fill_strided_kernel<uint16_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(fill_strided_kernel<uint32_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+    default: hipLaunchKernelGGL(fill_strided_kernel<uint64_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+  }
+  THIN_LAUNCH_CHECK("fill");
+  return THIN_OK;
 }

@@ -393,6 +393,115 @@ __global__ __launch_bounds__(kThreads) void nchw_up_kernel(NchwUpPlan p) {
   }
 }
 
+// ============================================================ max pool
+// Stride-1 max pool with an odd k x k window and "same" padding (taps outside
+// the plane are skipped, i.e. -inf).  A thread owns one pixel vector (V
+// values at one (plane, x): 8 channels of an NC1HWC0 pixel, or one NCHW
+// element) and walks a chunk of output rows, keeping the horizontal maxima of
+// the last k input rows in registers; output row y is the vertical max of
+// those k maxima.  Both passes keep the first strictly greater value, so the
+// selected value is the first maximum in row-major window order -- the one
+// PyTorch CPU's max_pool2d keeps (a +0/-0 tie resolves the same way).  A NaN
+// in the window gives NaN.
+struct PoolPlan {
+  const char* x;
+  char* y;
+  int64_t xs[4], ys[4];   // element strides of (n, c, h, w); NC1HWC0 adds the C0 part as V elements
+  uint32_t c, h, w;       // channels (or channel blocks), height, width
+  uint32_t parts;         // pixel vectors per pixel: 2 for NC1HWC0, 1 for NCHW
+  uint32_t rows;          // output rows per thread
+  uint32_t units;         // planes * chunks * w * parts
+  FastDiv div_parts, div_w, div_chunks, div_c;
+};
+
+template <typename T, int V>
+struct alignas(sizeof(T) * V) PoolVec {
+  T e[V];
+};
+
+template <typename T, int V>
+__device__ __forceinline__ void keep_max(PoolVec<T, V>& m, const PoolVec<T, V>& v) {
+#pragma unroll
+  for (int j = 0; j < V; ++j)
+    if (v.e[j] > m.e[j] || v.e[j] != v.e[j]) m.e[j] = v.e[j];
+}
+
+template <typename T, int V, int K>
+__global__ __launch_bounds__(kThreads) void maxpool_kernel(PoolPlan p) {
+  constexpr int R = K / 2;
+  const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
+  if (u >= p.units) return;
+  uint32_t q = p.div_parts.div(u);
+  const uint32_t part = u - q * p.parts;
+  uint32_t r = p.div_w.div(q);
+  const uint32_t x = q - r * p.w;
+  const uint32_t plane = p.div_chunks.div(r);
+  const uint32_t chunk = r - plane * p.div_chunks.d;
+  const uint32_t n = p.div_c.div(plane), c = plane - n * p.c;
+  const T* xp = reinterpret_cast<const T*>(p.x) + n * p.xs[0] + c * p.xs[1] + (int64_t)part * V;
+  T* yp = reinterpret_cast<T*>(p.y) + n * p.ys[0] + c * p.ys[1] + (int64_t)part * V + (int64_t)x * p.ys[3];
+  const int y0 = (int)(chunk * p.rows);
+  const int y1 = min((int)p.h, y0 + (int)p.rows);
+  PoolVec<T, V> ninf;
+#pragma unroll
+  for (int j = 0; j < V; ++j) ninf.e[j] = (T)(-__builtin_inff());
+  // horizontal max of input row yy at column x (-inf outside the plane)
+  auto hmax = [&](int yy) {
+    PoolVec<T, V> m = ninf;
+    if (yy >= 0 && yy < (int)p.h) {
+      const T* row = xp + (int64_t)yy * p.xs[2];
+#pragma unroll
+      for (int dx = -R; dx <= R; ++dx) {
+        const int xx = (int)x + dx;
+        if (xx >= 0 && xx < (int)p.w) keep_max(m, *reinterpret_cast<const PoolVec<T, V>*>(row + (int64_t)xx * p.xs[3]));
+      }
+    }
+    return m;
+  };
+  PoolVec<T, V> hm[K];
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i) hm[i + 1] = hmax(y0 - R + i);
+  for (int y = y0; y < y1; ++y) {
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) hm[i] = hm[i + 1];
+    hm[K - 1] = hmax(y + R);
+    PoolVec<T, V> m = ninf;
+#pragma unroll
+    for (int i = 0; i < K; ++i) keep_max(m, hm[i]);
+    *reinterpret_cast<PoolVec<T, V>*>(yp + (int64_t)y * p.ys[2]) = m;
+  }
+}
+
+template <typename T, int V>
+thin_status launch_pool(PoolPlan& p, uint32_t planes, int kernel, hipStream_t stream) {
+  // rows per thread: enough threads to fill the chip, few halo rows
+  uint32_t rows = p.h;
+  const uint64_t cols = (uint64_t)planes * p.w * p.parts;
+  while (rows > 4 && cols * ((p.h + rows - 1) / rows) < 256u * 256u) rows = (rows + 1) / 2;
+  const uint32_t chunks = (p.h + rows - 1) / rows;
+  const uint64_t units = cols * chunks;
+  THIN_REQUIRE(units < (1ull << 31), THIN_ERR_UNSUPPORTED, "maxpool: tensor too large");
+  p.rows = rows;
+  p.units = (uint32_t)units;
+  p.div_parts = FastDiv::make(p.parts);
+  p.div_w = FastDiv::make(p.w);
+  p.div_chunks = FastDiv::make(chunks);
+  p.div_c = FastDiv::make(p.c);
+  const uint32_t grid = (uint32_t)((units + kThreads - 1) / kThreads);
+  switch (kernel) {
+#define THIN_POOLK(KK) \
+  case KK: hipLaunchKernelGGL((maxpool_kernel<T, V, KK>), dim3(grid), dim3(kThreads), 0, stream, p); break;
+    THIN_POOLK(1) THIN_POOLK(3) THIN_POOLK(5) THIN_POOLK(7) THIN_POOLK(9) THIN_POOLK(11) THIN_POOLK(13)
+    THIN_POOLK(15)
+#undef THIN_POOLK
+    default: break;
+  }
+  THIN_LAUNCH_CHECK("maxpool");
+  return THIN_OK;
+}
+
+bool pool_kernel_ok(int32_t k) { return k >= 1 && k <= 15 && (k & 1); }
+
 // ============================================================ pack / unpack
 // Per (n, c1, tile of kTile pixels): LDS tile [16][kTile] of halves.
 constexpr int kTile = 256;
@@ -756,4 +865,61 @@ extern "C" thin_status thin_pack_nc1hwc0(const thin_desc* x, const thin_desc* y,
 extern "C" thin_status thin_unpack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStream_t stream) {
   clear_error();
   return repack(y, x, false, stream);
+}
+
+extern "C" thin_status thin_maxpool_nc1hwc0(const thin_desc* x, int32_t kernel, const thin_desc* out,
+                                            hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(desc_valid(x) && desc_valid(out), THIN_ERR_INVALID, "maxpool: invalid descriptor");
+  THIN_REQUIRE(x->dtype == THIN_F16 && out->dtype == THIN_F16 && x->rank == 5 && x->sizes[4] == 16 &&
+               same_sizes(x, out), THIN_ERR_INVALID, "maxpool expects float16 NC1HWC0 x and out of one shape");
+  THIN_REQUIRE(pool_kernel_ok(kernel), THIN_ERR_INVALID, "maxpool kernel must be an odd integer in [1, 15]");
+  if (numel(out) == 0) return THIN_OK;
+  for (const thin_desc* d : {x, out})
+    THIN_REQUIRE(d->strides[4] == 1 && (d->sizes[3] == 1 || d->strides[3] == 16) &&
+                 reinterpret_cast<uintptr_t>(d->data) % 16 == 0 && d->strides[0] % 8 == 0 &&
+                 d->strides[1] % 8 == 0 && d->strides[2] % 8 == 0, THIN_ERR_UNSUPPORTED,
+                 "maxpool needs 16-byte aligned pixels (C0 dense, W stride 16)");
+  THIN_REQUIRE(x->sizes[2] < (1 << 30) && x->sizes[3] < (1 << 30), THIN_ERR_UNSUPPORTED, "maxpool: plane too large");
+  PoolPlan p;
+  memset(&p, 0, sizeof p);
+  p.x = static_cast<const char*>(x->data);
+  p.y = static_cast<char*>(out->data);
+  for (int d = 0; d < 4; ++d) {
+    p.xs[d] = x->strides[d];
+    p.ys[d] = out->strides[d];
+  }
+  p.xs[3] = p.ys[3] = 16;
+  p.c = (uint32_t)x->sizes[1];
+  p.h = (uint32_t)x->sizes[2];
+  p.w = (uint32_t)x->sizes[3];
+  p.parts = 2;
+  return launch_pool<_Float16, 8>(p, (uint32_t)(x->sizes[0] * x->sizes[1]), kernel, stream);
+}
+
+extern "C" thin_status thin_maxpool2d_nchw(const thin_desc* x, int32_t kernel, const thin_desc* out,
+                                           hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(desc_valid(x) && desc_valid(out), THIN_ERR_INVALID, "maxpool2d: invalid descriptor");
+  THIN_REQUIRE((x->dtype == THIN_F16 || x->dtype == THIN_F32) && out->dtype == x->dtype && x->rank == 4 &&
+               same_sizes(x, out), THIN_ERR_INVALID, "maxpool2d expects float16/float32 NCHW x and out of one shape");
+  THIN_REQUIRE(pool_kernel_ok(kernel), THIN_ERR_INVALID, "maxpool2d kernel must be an odd integer in [1, 15]");
+  if (numel(out) == 0) return THIN_OK;
+  THIN_REQUIRE(x->sizes[0] * x->sizes[1] < (1ll << 31) && x->sizes[2] < (1 << 30) && x->sizes[3] < (1 << 30),
+               THIN_ERR_UNSUPPORTED, "maxpool2d: tensor too large");
+  PoolPlan p;
+  memset(&p, 0, sizeof p);
+  p.x = static_cast<const char*>(x->data);
+  p.y = static_cast<char*>(out->data);
+  for (int d = 0; d < 4; ++d) {
+    p.xs[d] = x->strides[d];
+    p.ys[d] = out->strides[d];
+  }
+  p.c = (uint32_t)x->sizes[1];
+  p.h = (uint32_t)x->sizes[2];
+  p.w = (uint32_t)x->sizes[3];
+  p.parts = 1;
+  const uint32_t planes = (uint32_t)(x->sizes[0] * x->sizes[1]);
+  if (x->dtype == THIN_F16) return launch_pool<_Float16, 1>(p, planes, kernel, stream);
+  return launch_pool<float, 1>(p, planes, kernel, stream);
 }

@@ -1,6 +1,6 @@
 // thin_native_flow::upsample / maxpool (libflow_ops.so), mirroring
-// flow_ops.cpp:201-266 of the reference.  upsample takes any N (the reference
-// requires N=1, flow_ops.cpp:202); maxpool is outside this backend and raises.
+// flow_ops.cpp:201-266 of the reference.  Both take any N (the reference
+// requires N=1, flow_ops.cpp:202); maxpool takes odd kernels up to 15.
 #include "thin_runtime.h"
 
 #include <torch/library.h>
@@ -28,8 +28,16 @@ at::Tensor upsample(const at::Tensor& x) {
 
 at::Tensor maxpool(const at::Tensor& x, int64_t kernel) {
   check_blocked(x);
-  (void)kernel;
-  TORCH_CHECK(false, "thin_native_flow.maxpool is not provided by the MI355X tensor-library backend");
+  TORCH_CHECK(kernel >= 1 && kernel % 2 == 1, "maxpool kernel must be a positive odd integer");
+  TORCH_CHECK(kernel <= 15, "maxpool kernel above 15 is not supported");
+  TORCH_CHECK(x.size(1) > 0 && x.size(2) > 0 && x.size(3) > 0, "blocked spatial operators require positive C1/H/W");
+  select(x.device());
+  auto y = at::empty(x.sizes(), x.options().memory_format(c10::MemoryFormat::Contiguous));
+  if (!y.numel()) return y;
+  thin_desc xd = desc(x), yd = desc(y);
+  check(thin_maxpool_nc1hwc0(&xd, (int32_t)kernel, &yd, stream()), "thin_native_flow.maxpool");
+  after_launch();
+  return y;
 }
 
 }  // namespace blocked_flow

@@ -208,16 +208,53 @@ at::Tensor aten_upsample_nearest2d(const at::Tensor& input, at::IntArrayRef outp
   return upsample_nchw(input.detach(), "upsample_nearest2d");
 }
 
+// ------------------------------------------------------------------ max pool
+// NCHW stride-1 max pool (backend.cpp:245-266, k5) through thin_maxpool2d_nchw.
+at::Tensor maxpool_nchw(const at::Tensor& x, int64_t kernel, const char* what) {
+  TORCH_CHECK(!x.requires_grad() || !c10::GradMode::is_enabled(), what, " is inference-only");
+  TORCH_CHECK(x.device().type() == kDevice, what, " requires an NPU tensor");
+  TORCH_CHECK(x.dim() == 4 && x.size(1) > 0 && x.size(2) > 0 && x.size(3) > 0, what,
+              " requires NCHW with positive C/H/W");
+  TORCH_CHECK(float_type(x), what, " supports float32 and float16");
+  select(x.device());
+  auto y = at::empty(x.sizes(), x.options().memory_format(c10::MemoryFormat::Contiguous));
+  if (!y.numel()) return y;
+  thin_desc xd = desc(x), yd = desc(y);
+  check(thin_maxpool2d_nchw(&xd, (int32_t)kernel, &yd, stream()), what);
+  after_launch();
+  return y;
+}
+
+int64_t square(at::IntArrayRef values, const char* name) {
+  TORCH_CHECK(values.size() == 1 || values.size() == 2, "thin aten: ", name, " must have one or two elements");
+  TORCH_CHECK(values.size() == 1 || values[0] == values[1], "thin aten: asymmetric ", name, " is unsupported");
+  return values[0];
+}
+
+// aten_adapter.cpp:61-80: k5/s1/p2/d1 only; indices are a zero placeholder.
+std::tuple<at::Tensor, at::Tensor> max_pool2d_with_indices(const at::Tensor& input, at::IntArrayRef kernel,
+                                                           at::IntArrayRef stride, at::IntArrayRef padding,
+                                                           at::IntArrayRef dilation, bool ceil_mode) {
+  TORCH_CHECK(square(kernel, "kernel_size") == 5 && (stride.empty() ? 5 : square(stride, "stride")) == 1 &&
+                  square(padding, "padding") == 2 && square(dilation, "dilation") == 1 && !ceil_mode,
+              "thin aten maxpool supports only k5/s1/p2/d1, ceil_mode=False");
+  trace("aten::max_pool2d_with_indices", "thin_maxpool2d_nchw (indices=zeros placeholder)");
+  auto values = maxpool_nchw(input.detach(), 5, "max_pool2d");
+  auto indices = at::empty(values.sizes(), values.options().dtype(at::kLong));
+  if (indices.numel()) {
+    thin_desc id = desc(indices);
+    check(thin_fill(&id, 0.0, 0, stream()), "zero placeholder indices");
+    after_launch();
+  }
+  return {values, indices};
+}
+
 // ------------------------------------------------------------------ rejects
-// The convolution / pooling / bmm family is not part of this backend: callers
-// get the reference's "thin aten" style error rather than a CPU fallback.
+// The convolution / bmm family is not part of this backend: callers get the
+// reference's "thin aten" style error rather than a CPU fallback.
 at::Tensor convolution(const at::Tensor&, const at::Tensor&, const std::optional<at::Tensor>&, at::IntArrayRef,
                        at::IntArrayRef, at::IntArrayRef, bool, at::IntArrayRef, int64_t) {
   TORCH_CHECK(false, "thin aten convolution is not provided by the MI355X tensor-library backend");
-}
-std::tuple<at::Tensor, at::Tensor> max_pool2d_with_indices(const at::Tensor&, at::IntArrayRef, at::IntArrayRef,
-                                                           at::IntArrayRef, at::IntArrayRef, bool) {
-  TORCH_CHECK(false, "thin aten maxpool is not provided by the MI355X tensor-library backend");
 }
 
 // ------------------------------------------------------------------ thin_backend::
@@ -236,6 +273,7 @@ at::Tensor tb_sigmoid(const at::Tensor& x) {
   return unary_out(x, THIN_SIGMOID, "sigmoid");
 }
 at::Tensor tb_upsample(const at::Tensor& x) { return upsample_nchw(x, "upsample_nearest2d"); }
+at::Tensor tb_maxpool2d(const at::Tensor& x) { return maxpool_nchw(x, 5, "maxpool2d"); }
 at::Tensor tb_unsupported1(const at::Tensor&) {
   TORCH_CHECK(false, "thin_backend: this operator is not provided by the MI355X tensor-library backend");
 }
@@ -397,7 +435,7 @@ TORCH_LIBRARY_IMPL(thin_backend, PrivateUse1, m) {
   m.impl("conv2d_fused", TORCH_FN(thin_ops::tb_conv_fused));
   m.impl("add", TORCH_FN(thin_ops::tb_add));
   m.impl("sigmoid", TORCH_FN(thin_ops::tb_sigmoid));
-  m.impl("maxpool2d", TORCH_FN(thin_ops::tb_unsupported1));
+  m.impl("maxpool2d", TORCH_FN(thin_ops::tb_maxpool2d));
   m.impl("upsample_nearest2d", TORCH_FN(thin_ops::tb_upsample));
   m.impl("conv2d", TORCH_FN(thin_ops::tb_conv_unsupported));
   m.impl("nms", TORCH_FN(thin_ops::tb_nms));

@@ -384,7 +384,7 @@ at::Tensor& copy_(at::Tensor& dst, const at::Tensor& src_in, bool non_blocking) 
 }
 
 // ------------------------------------------------------------------ host constants
-// decode.cpp:6-34: arange / fill_ computed on the CPU, then uploaded.
+// decode.cpp:6-34: arange computed on the CPU and uploaded; fill_ on the device.
 namespace {
 
 at::Tensor& arange_out(const at::Scalar& start, const at::Scalar& end, const at::Scalar& step, at::Tensor& out) {
@@ -400,9 +400,15 @@ at::Tensor& arange_out(const at::Scalar& start, const at::Scalar& end, const at:
 
 at::Tensor& arange_end_out(const at::Scalar& end, at::Tensor& out) { return arange_out(0, end, 1, out); }
 
+// fill_ / zero_ run the thin_fill kernel on the device (any strides; capture-safe).
 at::Tensor& fill(at::Tensor& out, const at::Scalar& value) {
-  auto constant = at::full(out.sizes(), value, out.options().device(at::kCPU));
-  return copy_(out, constant, false);
+  if (!out.numel()) return out;
+  select(out.device());
+  thin_desc od = desc(out);
+  const bool fp = at::isFloatingType(out.scalar_type());
+  check(thin_fill(&od, fp ? value.toDouble() : 0.0, fp ? 0 : value.toLong(), stream()), "fill_");
+  after_launch();
+  return out;
 }
 
 at::Tensor& zero(at::Tensor& out) { return fill(out, 0); }
