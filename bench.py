@@ -239,6 +239,18 @@ def op_maxpool(capi, dev, n, rotate=True):
     return (lambda st: capi.maxpool_nc1hwc0(st[0], 5, out=st[1])), sets, algo
 
 
+def op_decode(capi, dev, n, rotate=True):
+    """Anchor-free head decode: DFL [n,64,8400] + sigmoid [n,80,8400] -> [n,84,8400]."""
+    a = 8400
+    algo = n * a * 2 * (64 + 80 + 84)
+    g = torch.Generator(device=dev).manual_seed(6)
+    sets = rotated(lambda i: ((torch.randn((n, 64, a), generator=g, device=dev) * 3).half(),
+                              (torch.randn((n, 80, a), generator=g, device=dev) * 2 - 4).half(),
+                              torch.empty((n, 84, a), dtype=torch.float16, device=dev)), algo, rotate)
+    shapes, strides = [(80, 80), (40, 40), (20, 20)], [8.0, 16.0, 32.0]
+    return (lambda st: capi.detect_decode(st[0], st[1], shapes, strides, out=st[2])), sets, algo
+
+
 def op_select(capi, dev, layout, rotate=False):
     """C5 NMS-free top-300 of [1,8400,84] (latency-bound: report us)."""
     from tests.selection_fixtures import c5_selection_input  # input generator, shared with the tests
@@ -272,6 +284,7 @@ def op_rows(capi, dev):
         rows.append(("sigmoid_80x8400", "C4", n, lambda r, n=n: op_sigmoid(capi, dev, n, r)))
         rows.append(("softmax_4x400x400", "C5", n, lambda r, n=n: op_softmax(capi, dev, n, r)))
         rows.append(("maxpool_k5_256x20x20", "SPPF", n, lambda r, n=n: op_maxpool(capi, dev, n, r)))
+        rows.append(("detect_decode_64+80x8400", "C4", n, lambda r, n=n: op_decode(capi, dev, n, r)))
     for layout in ("contiguous", "transposed"):
         rows.append((f"detection_select_{layout}", "C5", 1, lambda r, l=layout: op_select(capi, dev, l)))
     return rows

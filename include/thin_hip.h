@@ -219,6 +219,21 @@ typedef struct thin_select_trace {
   void* labels;
 } thin_select_trace;
 
+/* Anchor-free detect-head decode in one launch: the DFL expectation of
+ * boxes [B,64,A] (bit-identical to thin_dfl_expect with fp16 output), the
+ * distances applied to the per-level grid cell centres (x + 0.5, y + 0.5) as
+ * lower = centre - d[0:2], upper = centre + d[2:4], scaled by the level stride
+ * as xyxy (lower, upper) or xywh ((lower+upper)/2, upper-lower), each step one
+ * correctly rounded fp16 operation; then sigmoid(scores [B,nc,A])
+ * (bit-identical to thin_unary SIGMOID).  out [B,4+nc,A] fp16 is the
+ * detection-selection input.  level_hw holds `levels` (h, w) pairs in anchor
+ * order (sum h*w = A), level_stride their strides (rounded to fp16).  Replaces
+ * the decode chain of anchorfree_predictions (whole_blocked.py:118-146;
+ * YOLO26.md:30-38). */
+thin_status thin_detect_decode(const thin_desc* boxes, const thin_desc* scores, const int32_t* level_hw,
+                               const double* level_stride, int32_t levels, int32_t xywh, const thin_desc* out,
+                               hipStream_t stream);
+
 /* Bytes of device workspace thin_detection_select needs for these sizes.
  * Replaces the intermediate tensors the reference allocates per call
  * (selection_flow.cpp:445-466: maxima, gathered, indices, values, records). */

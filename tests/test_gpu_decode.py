@@ -1,0 +1,90 @@
+"""Detect-head decode (whole_blocked.py:118-146) on the GPU.
+
+The fused kernel must equal, bit for bit, the composition of entries pinned
+elsewhere: thin_dfl_expect (fp16 distances) -> the oracle's fp16 box steps ->
+and thin_unary SIGMOID for the scores.  Against the full CPU oracle the boxes
+differ only through the DFL expectation's 1e-3 relative bar."""
+import pytest
+import torch
+
+from oracle import detect as dt
+from oracle import elementwise as ew
+from oracle.numerics import assert_ulp, bits_equal
+from tests.helpers import normal16
+
+pytestmark = pytest.mark.gpu
+
+YOLO = ([(80, 80), (40, 40), (20, 20)], [8.0, 16.0, 32.0])
+ODD = ([(3, 5), (2, 3)], [8.0, 16.0])
+
+
+def inputs(b, nc, shapes, seed):
+    a = sum(h * w for h, w in shapes)
+    return normal16((b, 64, a), seed, std=3.0), normal16((b, nc, a), seed + 1, mean=-4.0, std=2.0)
+
+
+def composed(capi, gpu, boxes, scores, shapes, strides, xywh):
+    distance = capi.dfl_expect(boxes.to(gpu)).cpu()
+    return torch.cat((dt.box_decode(distance, shapes, strides, xywh),
+                      capi.unary(capi.SIGMOID, scores.to(gpu)).cpu()), 1)
+
+
+@pytest.mark.parametrize("xywh", [False, True])
+@pytest.mark.parametrize("case", ["yolo", "odd"])
+def test_decode_equals_composition(gpu, xywh, case):
+    from thintnpu_amd import capi
+    shapes, strides = YOLO if case == "yolo" else ODD
+    boxes, scores = inputs(2, 80 if case == "yolo" else 3, shapes, 7)
+    got = capi.detect_decode(boxes.to(gpu), scores.to(gpu), shapes, strides, xywh).cpu()
+    want = composed(capi, gpu, boxes, scores, shapes, strides, xywh)
+    assert bits_equal(got, want)
+    ref = dt.detect_decode(boxes, scores, shapes, strides, xywh)
+    assert_ulp(got[:, 4:], ref[:, 4:], 2, "scores")
+    scale = dt.grid(shapes, strides)[1]
+    assert ((got[:, :4].float() - ref[:, :4].float()).abs() <= scale.float() * 0.05).all()
+
+
+def test_decode_views_and_specials(gpu):
+    from thintnpu_amd import capi
+    shapes, strides = YOLO
+    a = 8400
+    head = torch.cat(inputs(2, 80, shapes, 11), 1)        # [2, 144, A]: boxes then scores
+    head[0, 5, 17] = float("nan")
+    head[1, 20, 33] = float("inf")
+    head[1, 40:56, 100] = float("-inf")
+    head[0, 64 + 3, 9] = float("nan")
+    head[1, 64 + 7, 10] = float("-inf")
+    hd = head.to(gpu)
+    parent = torch.zeros((2, 84, a + 8), dtype=torch.float16, device=gpu)
+    capi.detect_decode(hd[:, :64], hd[:, 64:], shapes, strides, False, out=parent[..., :a])
+    got = parent.cpu()
+    want = composed(capi, gpu, head[:, :64].contiguous(), head[:, 64:].contiguous(), shapes, strides, False)
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got[..., :a]), nan)
+    assert bits_equal(got[..., :a][~nan], want[~nan])
+    assert not got[..., a:].any()
+
+
+def test_decode_npu_to_selection(gpu):
+    """thin_fused.detect_decode -> thin_native_flow.detection_select on the
+    production transposed view, eager == captured replay, bit-exact vs oracle."""
+    import thin_backend
+    from thin_backend.graph import CapturedForward
+    from oracle import selection as sel
+    thin_backend.load_flow_libraries()
+    npu = torch.device("npu:0")
+    shapes, strides = YOLO
+    boxes, scores = inputs(1, 80, shapes, 21)
+    with torch.inference_mode():
+        b, s = boxes.to(npu), scores.to(npu)
+
+        def forward(_=None):
+            decoded = torch.ops.thin_fused.detect_decode(b, s, [v for hw in shapes for v in hw], strides, False)
+            return torch.ops.thin_native_flow.detection_select(decoded.transpose(1, 2), 300, False)
+        eager = forward().cpu()
+        decoded = torch.ops.thin_fused.detect_decode(b, s, [v for hw in shapes for v in hw], strides, False).cpu()
+        assert bits_equal(eager, sel.select(decoded.transpose(1, 2), 300, False)["output"])
+        graph = CapturedForward(forward, b)
+        for _ in range(3):
+            assert bits_equal(graph.replay().cpu(), eager)
+        graph.close()

@@ -84,6 +84,7 @@ def lib() -> ctypes.CDLL:
             "thin_maxpool_nc1hwc0": [P, i32, P, vp],
             "thin_maxpool2d_nchw": [P, i32, P, vp],
             "thin_fill": [P, f64, i64, vp],
+            "thin_detect_decode": [P, P, ctypes.POINTER(i32), ctypes.POINTER(f64), i32, i32, P, vp],
             "thin_detection_select": [P, i64, i32, vp, vp, ctypes.c_size_t,
                                       ctypes.POINTER(ThinSelectTrace), vp],
         }
@@ -279,6 +280,21 @@ def dfl_expect(x, out_dtype=None, out=None, stream=None):
     n, c, a = x.shape
     out = torch.empty((n, c // 16, a), dtype=out_dtype or x.dtype, device=x.device) if out is None else out
     _call("thin_dfl_expect", _ref(desc(x)), _ref(desc(out)), _stream(stream))
+    return out
+
+
+def detect_decode(boxes, scores, shapes, strides, xywh: bool = False, out=None, stream=None):
+    """Anchor-free head decode: [B,64,A] box logits + [B,nc,A] class logits ->
+    [B,4+nc,A] fp16 (boxes by DFL + grid + stride, scores by sigmoid).
+    shapes: per-level (h, w); strides: per-level stride."""
+    b, _, a = boxes.shape
+    nc = scores.shape[1]
+    out = torch.empty((b, 4 + nc, a), dtype=torch.float16, device=boxes.device) if out is None else out
+    levels = len(shapes)
+    hw = (ctypes.c_int32 * (2 * levels))(*[int(v) for hw_ in shapes for v in hw_])
+    st = (ctypes.c_double * levels)(*[float(v) for v in strides])
+    _call("thin_detect_decode", _ref(desc(boxes)), _ref(desc(scores)), hw, st, levels, int(xywh),
+          _ref(desc(out)), _stream(stream))
     return out
 
 

@@ -119,6 +119,77 @@ __device__ __forceinline__ float fast_exp(float x) {
 }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
+// Sigmoid for fp16 outputs (shared by the elementwise and detect-decode
+// kernels so that both produce the same bits).
+__device__ __forceinline__ float sigmoid_fast(float x) { return fast_rcp(1.0f + fast_exp_neg(x)); }
+
+// DFL expectation of V adjacent anchors: sum_i i * softmax_i(bins[i][j]) over
+// the 16 bins of one box side.  The bin max only stabilises the exponentials
+// (plain max: a NaN bin, a +inf bin or an all -inf side already makes the sum
+// NaN, as the CPU softmax then expectation does).  FAST (fp16 results):
+// e = exp2(x*log2e - m*log2e) as one fma (an error in the common term scales
+// every e_i alike and cancels in w/s) and w * 1/s; otherwise expf and an IEEE
+// division.
+template <int V, bool FAST>
+__device__ __forceinline__ void dfl_side(const _Float16 (&bins)[16][V], float (&r)[V]) {
+  typedef _Float16 hv __attribute__((ext_vector_type(2)));
+  float m[V];
+  if constexpr (V == 2) {
+    hv mv = {bins[0][0], bins[0][1]};
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mv = __builtin_elementwise_max(mv, (hv){bins[i][0], bins[i][1]});
+    m[0] = (float)mv[0];
+    m[1] = (float)mv[1];
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      m[j] = (float)bins[0][j];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) m[j] = fmaxf(m[j], (float)bins[i][j]);
+    }
+  }
+  constexpr float kLog2e = 1.4426950408889634f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const float ml = m[j] * kLog2e;
+    float s = 0.f, w = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float x = (float)bins[i][j];
+      const float e = FAST ? __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -ml)) : expf(x - m[j]);
+      s += e;
+      w += e * (float)i;
+    }
+    if (FAST) {
+      // Materialise the fp32 quotient: otherwise the backend may fold the
+      // later fp16 conversion into a single-rounding v_fma_mixlo_f16 in one
+      // kernel and not in another, and the kernels sharing this function
+      // would disagree by an ulp on halfway cases.
+      float q = w * fast_rcp(s);
+      __asm__ volatile("" : "+v"(q));
+      r[j] = q;
+    } else {
+      r[j] = w / s;
+    }
+  }
+}
+
+// Loads the 16 bins (row stride xc) of V adjacent anchors starting at xp.
+template <int V>
+__device__ __forceinline__ void dfl_load(const _Float16* xp, int64_t xc, _Float16 (&bins)[16][V]) {
+  typedef _Float16 hv __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (V == 2) {
+      const hv b = *reinterpret_cast<const hv*>(xp + i * xc);
+      bins[i][0] = b[0];
+      bins[i][1] = b[1];
+    } else {
+      bins[i][0] = xp[i * xc];
+    }
+  }
+}
+
 // Sum / max across the 64 lanes of a wavefront (all lanes get the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -58,7 +58,7 @@ template <typename T> __device__ __forceinline__ T from_f(float v) { return (T)v
 // (sigmoid.cpp:30-36 and elementwise.cpp:76-86 compute the same formulas).
 template <typename T> __device__ __forceinline__ float sigmoid_f(float x);
 template <> __device__ __forceinline__ float sigmoid_f<_Float16>(float x) {
-  return fast_rcp(1.0f + fast_exp_neg(x));
+  return dev::sigmoid_fast(x);
 }
 template <> __device__ __forceinline__ float sigmoid_f<float>(float x) {
   return 1.0f / (1.0f + expf(-x));

@@ -254,13 +254,9 @@ struct DflPlan {
   FastDiv div_avecs;
 };
 
-// The bin maximum only stabilises the exponentials, so it is taken without
-// NaN propagation (in packed fp16 for two anchors, where max is exact): a NaN
-// bin, a +inf bin (inf - inf) or an all -inf side (-inf - -inf) already makes
-// the sum, and so the result, NaN -- as CPU's softmax then expectation does.
-// FAST (fp16 output): e = exp2(x*log2e - m*log2e) as one fma (an error in the
-// common term m*log2e scales every e_i alike and cancels in w/s) and w * 1/s;
-// the fp32 output uses expf and an IEEE division.
+// Thread per V (1 or 2) adjacent anchors of one box side; the math is
+// dev::dfl_side (shared with the detect-decode kernel, so both give the same
+// bits).
 template <typename TO, int V, bool FAST>
 __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
   static_assert(V == 1 || V == 2, "one or two anchors per thread");
@@ -270,51 +266,115 @@ __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
   const uint32_t a0 = (u - side * p.avecs) * V;
   const uint32_t n = side >> 2, sd = side & 3u;
   const _Float16* xp = p.x + n * p.xn + (int64_t)(sd * 16) * p.xc + (int64_t)a0 * p.xa;
-  typedef _Float16 hv __attribute__((ext_vector_type(2)));
   _Float16 bins[16][V];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if (V == 2) {
-      const hv b = *reinterpret_cast<const hv*>(xp + i * p.xc);
-      bins[i][0] = b[0];
-      bins[i][V - 1] = b[1];
-    } else {
-      bins[i][0] = xp[i * p.xc];
-    }
-  }
-  float m[V];
-  if (V == 2) {
-    hv mv = {bins[0][0], bins[0][V - 1]};
-#pragma unroll
-    for (int i = 1; i < 16; ++i) mv = __builtin_elementwise_max(mv, (hv){bins[i][0], bins[i][V - 1]});
-    m[0] = (float)mv[0];
-    m[V - 1] = (float)mv[1];
-  } else {
-    m[0] = (float)bins[0][0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i) m[0] = fmaxf(m[0], (float)bins[i][0]);
-  }
-  constexpr float kLog2e = 1.4426950408889634f;
+  dev::dfl_load<V>(xp, p.xc, bins);
   float r[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) {
-    const float ml = m[j] * kLog2e;
-    float s = 0.f, w = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float x = (float)bins[i][j];
-      const float e = FAST ? __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -ml)) : expf(x - m[j]);
-      s += e;
-      w += e * (float)i;
-    }
-    r[j] = FAST ? w * __builtin_amdgcn_rcpf(s) : w / s;
-  }
+  dev::dfl_side<V, FAST>(bins, r);
   TO* op = static_cast<TO*>(p.out) + n * p.on + (int64_t)sd * p.os + (int64_t)a0 * p.oa;
-  if (V == 2) {
+  if constexpr (V == 2) {
     typedef TO ov __attribute__((ext_vector_type(2)));
-    *reinterpret_cast<ov*>(op) = (ov){(TO)r[0], (TO)r[V - 1]};
+    *reinterpret_cast<ov*>(op) = (ov){(TO)r[0], (TO)r[1]};
   } else {
     op[0] = (TO)r[0];
+  }
+}
+
+// ---------------------------------------------------------------- detect decode
+// Anchor-free detect head in one launch (whole_blocked.py:118-146):
+//   distance = DFL(boxes)                      [B,4,A] fp16 (dev::dfl_side)
+//   lower = anchor - distance[:, :2], upper = anchor + distance[:, 2:]
+//   xyxy: (lower, upper) * stride;  xywh: ((lower+upper)/2, upper-lower) * stride
+//   out = cat(boxes, sigmoid(scores))          [B,4+nc,A] fp16
+// Each arithmetic step is one correctly rounded fp16 operation, as the
+// reference's fp16 tensor ops are.  Anchors are the per-level grid cell
+// centres (x + 0.5, y + 0.5) in fp16, anchor index = level start + y*w + x.
+// Blocks [0, box_blocks) decode boxes: a thread takes one axis (x or y) of V
+// adjacent anchors and so the box sides axis and axis+2.  The remaining blocks
+// apply the sigmoid to the class logits, 8 per thread when rows are aligned.
+constexpr int kMaxLevels = 8;
+
+struct DecodePlan {
+  const _Float16* boxes;  // [B,64,A]
+  const _Float16* scores; // [B,nc,A]
+  _Float16* out;          // [B,4+nc,A]
+  int64_t bb, bc, ba, sb, sc, sa, ob, oc, oa;  // element strides
+  uint32_t levels;
+  uint32_t start[kMaxLevels + 1];
+  FastDiv width[kMaxLevels];
+  uint16_t stride_bits[kMaxLevels];  // fp16 stride per level
+  uint32_t apairs;        // A / VB
+  uint32_t box_units;     // B * 2 * apairs
+  uint32_t box_blocks;
+  uint32_t nc;
+  uint32_t svecs;         // A / VS
+  uint32_t score_units;   // B * nc * svecs
+  FastDiv div_apairs, div_svecs, div_nc;
+  int32_t xywh;
+};
+
+__device__ __forceinline__ _Float16 h_from_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
+
+template <int VB, int VS>
+__global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
+  if (blockIdx.x < p.box_blocks) {
+    const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
+    if (u >= p.box_units) return;
+    const uint32_t ba_ = p.div_apairs.div(u);          // b * 2 + axis
+    const uint32_t a0 = (u - ba_ * p.apairs) * VB;
+    const uint32_t b = ba_ >> 1, axis = ba_ & 1u;
+    const _Float16* xb = p.boxes + b * p.bb + (int64_t)a0 * p.ba;
+    _Float16 bins[16][VB];
+    float lo[VB], hi[VB];
+    dev::dfl_load<VB>(xb + (int64_t)(axis * 16) * p.bc, p.bc, bins);
+    dev::dfl_side<VB, true>(bins, lo);
+    dev::dfl_load<VB>(xb + (int64_t)((axis + 2) * 16) * p.bc, p.bc, bins);
+    dev::dfl_side<VB, true>(bins, hi);
+    _Float16 first[VB], second[VB];
+#pragma unroll
+    for (int j = 0; j < VB; ++j) {
+      const uint32_t a = a0 + j;
+      uint32_t l = 0;
+      while (l + 1 < p.levels && a >= p.start[l + 1]) ++l;
+      const uint32_t local = a - p.start[l];
+      const uint32_t y = p.width[l].div(local), x = local - y * p.width[l].d;
+      const _Float16 centre = (_Float16)(float)(axis ? y : x) + (_Float16)0.5f;
+      const _Float16 stride = h_from_bits(p.stride_bits[l]);
+      const _Float16 lower = centre - (_Float16)lo[j];
+      const _Float16 upper = centre + (_Float16)hi[j];
+      if (p.xywh) {
+        first[j] = ((lower + upper) / (_Float16)2.0f) * stride;
+        second[j] = (upper - lower) * stride;
+      } else {
+        first[j] = lower * stride;
+        second[j] = upper * stride;
+      }
+    }
+    _Float16* o = p.out + b * p.ob + (int64_t)a0 * p.oa;
+    if constexpr (VB == 2) {
+      typedef _Float16 hv __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<hv*>(o + (int64_t)axis * p.oc) = (hv){first[0], first[1]};
+      *reinterpret_cast<hv*>(o + (int64_t)(axis + 2) * p.oc) = (hv){second[0], second[1]};
+    } else {
+      o[(int64_t)axis * p.oc] = first[0];
+      o[(int64_t)(axis + 2) * p.oc] = second[0];
+    }
+    return;
+  }
+  const uint32_t v = (blockIdx.x - p.box_blocks) * kThreads + threadIdx.x;
+  if (v >= p.score_units) return;
+  const uint32_t row = p.div_svecs.div(v);               // b * nc + c
+  const uint32_t a0 = (v - row * p.svecs) * VS;
+  const uint32_t b = p.div_nc.div(row), c = row - b * p.nc;
+  const _Float16* sp = p.scores + b * p.sb + (int64_t)c * p.sc + (int64_t)a0 * p.sa;
+  _Float16* op = p.out + b * p.ob + (int64_t)(4 + c) * p.oc + (int64_t)a0 * p.oa;
+  if constexpr (VS == 8) {
+    const dev::h8 x = *reinterpret_cast<const dev::h8*>(sp);
+    dev::h8 y;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = (_Float16)dev::sigmoid_fast((float)x[j]);
+    *reinterpret_cast<dev::h8*>(op) = y;
+  } else {
+    op[0] = (_Float16)dev::sigmoid_fast((float)sp[0]);
   }
 }
 
@@ -492,5 +552,71 @@ extern "C" thin_status thin_dfl_expect(const thin_desc* x, const thin_desc* out,
     else hipLaunchKernelGGL((dfl_expect_kernel<float, 1, false>), dim3(grid), dim3(kThreads), 0, stream, p);
   }
   THIN_LAUNCH_CHECK("dfl_expect");
+  return THIN_OK;
+}
+
+extern "C" thin_status thin_detect_decode(const thin_desc* boxes, const thin_desc* scores, const int32_t* level_hw,
+                                          const double* level_stride, int32_t levels, int32_t xywh,
+                                          const thin_desc* out, hipStream_t stream) {
+  clear_error();
+  THIN_REQUIRE(desc_valid(boxes) && desc_valid(scores) && desc_valid(out), THIN_ERR_INVALID,
+               "detect_decode: invalid descriptor");
+  THIN_REQUIRE(boxes->dtype == THIN_F16 && scores->dtype == THIN_F16 && out->dtype == THIN_F16 &&
+               boxes->rank == 3 && scores->rank == 3 && out->rank == 3, THIN_ERR_INVALID,
+               "detect_decode takes float16 boxes [B,64,A], scores [B,nc,A] and out [B,4+nc,A]");
+  const int64_t B = boxes->sizes[0], A = boxes->sizes[2], nc = scores->sizes[1];
+  THIN_REQUIRE(boxes->sizes[1] == 64 && scores->sizes[0] == B && scores->sizes[2] == A && out->sizes[0] == B &&
+               out->sizes[1] == 4 + nc && out->sizes[2] == A, THIN_ERR_INVALID,
+               "detect_decode expects boxes [B,64,A], scores [B,nc,A], out [B,4+nc,A]");
+  THIN_REQUIRE(levels >= 1 && levels <= kMaxLevels && level_hw && level_stride, THIN_ERR_INVALID,
+               "detect_decode takes 1..%d levels", kMaxLevels);
+  DecodePlan p;
+  memset(&p, 0, sizeof p);
+  int64_t total = 0;
+  for (int l = 0; l < levels; ++l) {
+    THIN_REQUIRE(level_hw[2 * l] > 0 && level_hw[2 * l + 1] > 0, THIN_ERR_INVALID,
+                 "detect_decode: level sizes must be positive");
+    p.start[l] = (uint32_t)total;
+    p.width[l] = FastDiv::make((uint32_t)level_hw[2 * l + 1]);
+    const _Float16 st = (_Float16)(float)level_stride[l];
+    p.stride_bits[l] = __builtin_bit_cast(uint16_t, st);
+    total += (int64_t)level_hw[2 * l] * level_hw[2 * l + 1];
+  }
+  THIN_REQUIRE(total == A, THIN_ERR_INVALID, "detect_decode: level sizes cover %lld anchors, tensors have %lld",
+               (long long)total, (long long)A);
+  if (numel(out) == 0) return THIN_OK;
+  p.start[levels] = (uint32_t)total;
+  p.levels = (uint32_t)levels;
+  p.boxes = static_cast<const _Float16*>(boxes->data);
+  p.scores = static_cast<const _Float16*>(scores->data);
+  p.out = static_cast<_Float16*>(out->data);
+  p.bb = boxes->strides[0]; p.bc = boxes->strides[1]; p.ba = boxes->strides[2];
+  p.sb = scores->strides[0]; p.sc = scores->strides[1]; p.sa = scores->strides[2];
+  p.ob = out->strides[0]; p.oc = out->strides[1]; p.oa = out->strides[2];
+  p.nc = (uint32_t)nc;
+  p.xywh = xywh ? 1 : 0;
+  const bool vb = A % 2 == 0 && p.ba == 1 && p.oa == 1 && aligned(boxes->data, 4) && aligned(out->data, 4) &&
+                  p.bb % 2 == 0 && p.bc % 2 == 0 && p.ob % 2 == 0 && p.oc % 2 == 0;
+  const bool vs = A % 8 == 0 && p.sa == 1 && p.oa == 1 && aligned(scores->data, 16) && aligned(out->data, 16) &&
+                  p.sb % 8 == 0 && p.sc % 8 == 0 && p.ob % 8 == 0 && p.oc % 8 == 0;
+  const int VB = vb ? 2 : 1, VS = vs ? 8 : 1;
+  p.apairs = (uint32_t)(A / VB);
+  const uint64_t box_units = (uint64_t)B * 2 * p.apairs;
+  p.svecs = (uint32_t)(A / VS);
+  const uint64_t score_units = (uint64_t)B * nc * p.svecs;
+  THIN_REQUIRE(box_units < (1ull << 31) && score_units < (1ull << 31), THIN_ERR_UNSUPPORTED,
+               "detect_decode: tensors too large");
+  p.box_units = (uint32_t)box_units;
+  p.score_units = (uint32_t)score_units;
+  p.box_blocks = (uint32_t)((box_units + kThreads - 1) / kThreads);
+  p.div_apairs = FastDiv::make(p.apairs);
+  p.div_svecs = FastDiv::make(p.svecs);
+  p.div_nc = FastDiv::make((uint32_t)nc);
+  const uint32_t grid = p.box_blocks + (uint32_t)((score_units + kThreads - 1) / kThreads);
+  if (vb && vs) hipLaunchKernelGGL((detect_decode_kernel<2, 8>), dim3(grid), dim3(kThreads), 0, stream, p);
+  else if (vb) hipLaunchKernelGGL((detect_decode_kernel<2, 1>), dim3(grid), dim3(kThreads), 0, stream, p);
+  else if (vs) hipLaunchKernelGGL((detect_decode_kernel<1, 8>), dim3(grid), dim3(kThreads), 0, stream, p);
+  else hipLaunchKernelGGL((detect_decode_kernel<1, 1>), dim3(grid), dim3(kThreads), 0, stream, p);
+  THIN_LAUNCH_CHECK("detect_decode");
   return THIN_OK;
 }

@@ -393,6 +393,34 @@ at::Tensor dfl_expect(const at::Tensor& x, bool fp32_output) {
   return out;
 }
 
+// Anchor-free head decode (whole_blocked.py:118-146): shapes = flattened
+// per-level (h, w), strides = per-level strides.
+void decode_check(const at::Tensor& boxes, const at::Tensor& scores, at::IntArrayRef shapes,
+                  at::ArrayRef<double> strides) {
+  TORCH_CHECK(boxes.scalar_type() == at::kHalf && scores.scalar_type() == at::kHalf && boxes.dim() == 3 &&
+                  scores.dim() == 3 && boxes.size(1) == 64 && scores.size(0) == boxes.size(0) &&
+                  scores.size(2) == boxes.size(2),
+              "detect_decode expects float16 boxes [B,64,A] and scores [B,nc,A]");
+  TORCH_CHECK(shapes.size() % 2 == 0 && shapes.size() / 2 == strides.size() && !strides.empty() &&
+                  strides.size() <= 8,
+              "detect_decode expects (h, w) per level and one stride per level (1..8 levels)");
+}
+at::Tensor detect_decode(const at::Tensor& boxes, const at::Tensor& scores, at::IntArrayRef shapes,
+                         at::ArrayRef<double> strides, bool xywh) {
+  inference(boxes, "thin_fused.detect_decode");
+  inference(scores, "thin_fused.detect_decode");
+  decode_check(boxes, scores, shapes, strides);
+  select(boxes.device());
+  auto out = at::empty({boxes.size(0), 4 + scores.size(1), boxes.size(2)}, boxes.options());
+  std::vector<int32_t> hw(shapes.begin(), shapes.end());
+  std::vector<double> st(strides.begin(), strides.end());
+  thin_desc bd = desc(boxes), sd = desc(scores), od = desc(out);
+  check(thin_detect_decode(&bd, &sd, hw.data(), st.data(), (int32_t)st.size(), xywh ? 1 : 0, &od, stream()),
+        "thin detect_decode");
+  after_launch();
+  return out;
+}
+
 // Meta kernels of thin_fused: the shapes and dtypes of the device kernels.
 at::Tensor silu_add_meta(const at::Tensor& x, const at::Tensor& y) {
   TORCH_CHECK(float_type(x) && x.scalar_type() == y.scalar_type(), "silu_add requires matching float16/float32");
@@ -405,6 +433,11 @@ at::Tensor affine_silu_meta(const at::Tensor& x, const at::Tensor& s, const at::
 }
 at::Tensor upsample_cat_meta(at::TensorList xs, at::IntArrayRef upsample) {
   return at::empty(upsample_cat_sizes(xs, upsample), xs[0].options());
+}
+at::Tensor detect_decode_meta(const at::Tensor& boxes, const at::Tensor& scores, at::IntArrayRef shapes,
+                              at::ArrayRef<double> strides, bool) {
+  decode_check(boxes, scores, shapes, strides);
+  return at::empty({boxes.size(0), 4 + scores.size(1), boxes.size(2)}, boxes.options());
 }
 at::Tensor dfl_expect_meta(const at::Tensor& x, bool fp32_output) {
   TORCH_CHECK(x.scalar_type() == at::kHalf && x.dim() == 3 && x.size(1) == 64,
@@ -460,6 +493,7 @@ TORCH_LIBRARY(thin_fused, m) {
   m.def("affine_silu(Tensor x, Tensor scale, Tensor bias) -> Tensor");
   m.def("upsample_cat(Tensor[] tensors, int[] upsample) -> Tensor");
   m.def("dfl_expect(Tensor x, bool fp32_output=False) -> Tensor");
+  m.def("detect_decode(Tensor boxes, Tensor scores, int[] shapes, float[] strides, bool xywh=False) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(thin_fused, PrivateUse1, m) {
@@ -467,10 +501,11 @@ TORCH_LIBRARY_IMPL(thin_fused, PrivateUse1, m) {
   m.impl("affine_silu", TORCH_FN(thin_ops::affine_silu));
   m.impl("upsample_cat", TORCH_FN(thin_ops::upsample_cat));
   m.impl("dfl_expect", TORCH_FN(thin_ops::dfl_expect));
+  m.impl("detect_decode", TORCH_FN(thin_ops::detect_decode));
 }
 
 TORCH_LIBRARY_IMPL(thin_fused, AutogradPrivateUse1, m) {
-  for (const char* name : {"silu_add", "affine_silu", "upsample_cat", "dfl_expect"})
+  for (const char* name : {"silu_add", "affine_silu", "upsample_cat", "dfl_expect", "detect_decode"})
     m.impl(name, torch::CppFunction::makeFallthrough());
 }
 
@@ -479,4 +514,5 @@ TORCH_LIBRARY_IMPL(thin_fused, Meta, m) {
   m.impl("affine_silu", TORCH_FN(thin_ops::affine_silu_meta));
   m.impl("upsample_cat", TORCH_FN(thin_ops::upsample_cat_meta));
   m.impl("dfl_expect", TORCH_FN(thin_ops::dfl_expect_meta));
+  m.impl("detect_decode", TORCH_FN(thin_ops::detect_decode_meta));
 }
