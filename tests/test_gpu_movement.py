@@ -251,3 +251,13 @@ def test_fill(gpu):
         got = parent.cpu()
         assert torch.equal(torch.isnan(got.float()), torch.isnan(ref.float())) if dtype.is_floating_point else True
         assert torch.equal(got.nan_to_num(), ref.nan_to_num()) if dtype.is_floating_point else torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("c,h,w,k", [(16, 3, 300, 5), (16, 5, 130, 15), (32, 9, 64, 15), (16, 33, 7, 3)])
+def test_maxpool_wide_rows(gpu, c, h, w, k):
+    """Rows too wide for the LDS band (register form) and tall narrow planes."""
+    from thintnpu_amd import capi
+    x = pool_specials(to_blocked(normal16((2, c, h, w), w + k)))
+    check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"{c}x{h}x{w} k{k}")
+    y = pool_specials(normal16((1, 3, h, w * 5), k))
+    check_pool(capi.maxpool2d_nchw(y.to(gpu), k).cpu(), mv.maxpool_nchw(y, k), f"nchw {h}x{w * 5} k{k}")

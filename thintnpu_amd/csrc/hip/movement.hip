@@ -8,6 +8,8 @@
 // channel transpose of the repack.
 #include "common.h"
 
+#include <algorithm>
+
 #include <string.h>
 
 namespace thin {
@@ -412,6 +414,7 @@ struct PoolPlan {
   uint32_t rows;          // output rows per thread
   uint32_t units;         // planes * chunks * w * parts
   FastDiv div_parts, div_w, div_chunks, div_c;
+  FastDiv div_row;        // w * parts (LDS form)
 };
 
 template <typename T, int V>
@@ -472,9 +475,112 @@ __global__ __launch_bounds__(kThreads) void maxpool_kernel(PoolPlan p) {
   }
 }
 
+// LDS-tiled form: a block takes one plane band of `rows` output rows.  The
+// band's input rows plus the 2R halo rows are read once (coalesced) into LDS,
+// horizontal maxima go to a second LDS buffer, vertical maxima to HBM -- one
+// global round trip per block instead of one per output row.
+template <typename T, int V, int K>
+__global__ __launch_bounds__(kThreads) void maxpool_tile_kernel(PoolPlan p, uint32_t bands) {
+  constexpr int R = K / 2;
+  extern __shared__ __attribute__((aligned(16))) char pool_lds[];
+  typedef PoolVec<T, V> PV;
+  const uint32_t plane = blockIdx.x / bands, band = blockIdx.x - plane * bands;
+  const uint32_t n = p.div_c.div(plane), c = plane - n * p.c;
+  const int y0 = (int)(band * p.rows);
+  const int tile_rows = (int)p.rows + 2 * R;
+  const uint32_t row_vecs = p.w * p.parts;
+  const uint32_t tile = (uint32_t)tile_rows * row_vecs;
+  PV* in = reinterpret_cast<PV*>(pool_lds);
+  PV* hm = in + tile;
+  PV ninf;
+#pragma unroll
+  for (int j = 0; j < V; ++j) ninf.e[j] = (T)(-__builtin_inff());
+  const T* xp = reinterpret_cast<const T*>(p.x) + n * p.xs[0] + c * p.xs[1];
+  const uint32_t pshift = p.parts == 2 ? 1u : 0u;
+  // four loads in flight per thread before their LDS writes
+  constexpr int U = 4;
+  for (uint32_t i0 = threadIdx.x; i0 < tile; i0 += U * kThreads) {
+    PV v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = i0 + u * kThreads;
+      v[u] = ninf;
+      if (i < tile) {
+        const uint32_t rr = p.div_row.div(i), k = i - rr * row_vecs;
+        const uint32_t x = k >> pshift, part = k & pshift;
+        const int yy = y0 - R + (int)rr;
+        if (yy >= 0 && yy < (int)p.h)
+          v[u] = *reinterpret_cast<const PV*>(xp + (int64_t)yy * p.xs[2] + (int64_t)x * p.xs[3] + (int64_t)part * V);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * kThreads < tile) in[i0 + u * kThreads] = v[u];
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < tile; i += kThreads) {
+    const uint32_t rr = p.div_row.div(i), k = i - rr * row_vecs;
+    const uint32_t x = k >> pshift;
+    PV m = ninf;
+#pragma unroll
+    for (int dx = -R; dx <= R; ++dx) {
+      const int xx = (int)x + dx;
+      if (xx >= 0 && xx < (int)p.w) keep_max(m, in[i + dx * (int)p.parts]);
+    }
+    hm[i] = m;
+  }
+  __syncthreads();
+  T* yp = reinterpret_cast<T*>(p.y) + n * p.ys[0] + c * p.ys[1];
+  const uint32_t outs = p.rows * row_vecs;
+  for (uint32_t i = threadIdx.x; i < outs; i += kThreads) {
+    const uint32_t ry = p.div_row.div(i), k = i - ry * row_vecs;
+    const int y = y0 + (int)ry;
+    if (y >= (int)p.h) break;
+    const uint32_t x = k >> pshift, part = k & pshift;
+    PV m = ninf;
+#pragma unroll
+    for (int dy = 0; dy <= 2 * R; ++dy) keep_max(m, hm[(ry + dy) * row_vecs + k]);
+    *reinterpret_cast<PV*>(yp + (int64_t)y * p.ys[2] + (int64_t)x * p.ys[3] + (int64_t)part * V) = m;
+  }
+}
+
+constexpr size_t kPoolLdsBytes = 64 * 1024;
+
 template <typename T, int V>
 thin_status launch_pool(PoolPlan& p, uint32_t planes, int kernel, hipStream_t stream) {
-  // rows per thread: enough threads to fill the chip, few halo rows
+  const int R = kernel / 2;
+  const size_t row_bytes = (size_t)p.w * p.parts * sizeof(PoolVec<T, V>);
+  const uint64_t plane_rows = (uint64_t)planes * p.h;
+  // LDS form: band height for >= ~2048 blocks (several per CU to overlap the
+  // load round trip of one band with the max passes of another), within the
+  // LDS budget (in + hm); halo rows are re-read from L2
+  const size_t max_tile_rows = kPoolLdsBytes / (2 * row_bytes);
+  if (max_tile_rows > (size_t)(2 * R)) {
+    uint32_t rows = (uint32_t)((plane_rows + 2047) / 2048);
+    rows = std::max<uint32_t>(1u, std::min<uint32_t>(rows, p.h));
+    rows = std::min<uint32_t>(rows, (uint32_t)(max_tile_rows - 2 * R));
+    const uint32_t bands = (p.h + rows - 1) / rows;
+    const uint64_t blocks = (uint64_t)planes * bands;
+    THIN_REQUIRE(blocks < (1ull << 31), THIN_ERR_UNSUPPORTED, "maxpool: tensor too large");
+    p.rows = rows;
+    p.div_c = FastDiv::make(p.c);
+    p.div_row = FastDiv::make(p.w * p.parts);
+    const size_t lds = 2 * (size_t)(rows + 2 * R) * row_bytes;
+    switch (kernel) {
+#define THIN_POOLT(KK)                                                                                       \
+  case KK:                                                                                                    \
+    hipLaunchKernelGGL((maxpool_tile_kernel<T, V, KK>), dim3((uint32_t)blocks), dim3(kThreads), lds, stream, p, \
+                       bands);                                                                                \
+    break;
+      THIN_POOLT(1) THIN_POOLT(3) THIN_POOLT(5) THIN_POOLT(7) THIN_POOLT(9) THIN_POOLT(11) THIN_POOLT(13)
+      THIN_POOLT(15)
+#undef THIN_POOLT
+      default: break;
+    }
+    THIN_LAUNCH_CHECK("maxpool");
+    return THIN_OK;
+  }
+  // register form for rows too wide for LDS: rows per thread chosen to fill the chip
   uint32_t rows = p.h;
   const uint64_t cols = (uint64_t)planes * p.w * p.parts;
   while (rows > 4 && cols * ((p.h + rows - 1) / rows) < 256u * 256u) rows = (rows + 1) / 2;
