@@ -399,3 +399,50 @@ def test_aten_trace_and_process_hygiene(npu, capfd, monkeypatch):
         except (OSError, IndexError, ValueError):
             return None
     assert [p for p in os.listdir("/proc") if p.isdigit() and parent(p) == os.getpid()] == []
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_materialize_cases(npu, dtype):
+    """verify_materialize.py:15-74 restated: permute(0,2,1).contiguous() with
+    capture and changed-input replay, sliced / strided / expanded views, the
+    strided-concat grid and raw-bit transposes."""
+    from thin_backend.graph import CapturedForward
+    bits = lambda t: t.cpu().contiguous().view(torch.int16 if t.element_size() == 2 else torch.int32)  # noqa: E731
+    g = gen(913)
+    with torch.inference_mode():
+        for groups, channels, rows in ((1, 16, 16), (3, 16, 6400), (2, 32, 48), (4, 48, 400), (2, 7, 19),
+                                       (1, 85, 96)):
+            x = torch.randn(groups, channels, rows, generator=g).to(dtype)
+            forward = lambda value: value.permute(0, 2, 1).contiguous()  # noqa: E731
+            expected = forward(x)
+            assert torch.equal(bits(forward(x.to(npu))), bits(expected))
+            graph = CapturedForward(forward, x.to(npu))
+            assert torch.equal(bits(graph.replay()), bits(expected))
+            changed = (x * 0.5).to(npu)
+            assert torch.equal(bits(graph(changed)), bits(forward(changed)))
+            graph.close()
+        for shape in ((3, 128, 16), (2, 19, 7), (1, 32, 85), (4, 48, 32)):
+            x = torch.randn(shape, generator=g).to(dtype)
+            xn = x.to(npu)
+            for view in (lambda t: t[..., 2:4], lambda t: t[..., 4:], lambda t: t[:, ::2, ::2],
+                         lambda t: t[:, :1].expand(-1, 31, -1)):
+                assert torch.equal(bits(view(xn).contiguous()), bits(view(x).contiguous()))
+        for rows in (1, 7, 127, 128, 129, 6400):
+            for widths in ((2, 2, 12), (1, 7, 24), (3, 5, 8), (6, 10)):
+                sources = [torch.randn(rows, w, generator=g).to(dtype) for w in widths]
+                values = [s.to(npu) for s in sources]
+                want = torch.cat(sources, -1)
+                assert torch.equal(bits(torch.cat(values, -1)), bits(want))
+                graph = CapturedForward(lambda _: torch.cat(values, -1), values[0])
+                assert torch.equal(bits(graph.replay()), bits(want))
+                graph.close()
+        for mode, transform in (("sliced", lambda t: t[::3]), ("broadcast", lambda t: t[:1].expand(273, -1)),
+                                ("offset", lambda t: t[:, 1:])):
+            sources = [torch.randn(273, w + (mode == "offset"), generator=g).to(dtype) for w in (2, 2, 12)]
+            values = [transform(s.to(npu)) for s in sources]
+            assert torch.equal(bits(torch.cat(values, -1)), bits(torch.cat([transform(s) for s in sources], -1)))
+    raw = random_bits16((3, 32, 48), 913)
+    with torch.inference_mode():
+        assert bits_equal(raw.to(npu).transpose(1, 2).contiguous().cpu(), raw.transpose(1, 2).contiguous())
+        slices = [raw[..., :2].contiguous(), raw[..., 2:4].contiguous(), raw[..., 4:16].contiguous()]
+        assert bits_equal(torch.cat([s.to(npu) for s in slices], -1).cpu(), torch.cat(slices, -1))
