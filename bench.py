@@ -251,6 +251,14 @@ def op_decode(capi, dev, n, rotate=True):
     return (lambda st: capi.detect_decode(st[0], st[1], shapes, strides, out=st[2])), sets, algo
 
 
+def op_permute(capi, dev, n, rotate=True):
+    """Materialize NCHW [n,64,80,80] as NHWC: x.permute(0,2,3,1).contiguous()."""
+    algo = n * 64 * 80 * 80 * 2 * 2
+    sets = rotated(lambda i: (torch.randn((n, 64, 80, 80), device=dev).half(),
+                              torch.empty((n, 80, 80, 64), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.copy(st[0].permute(0, 2, 3, 1), st[1])), sets, algo
+
+
 def op_select(capi, dev, layout, rotate=False):
     """C5 NMS-free top-300 of [1,8400,84] (latency-bound: report us)."""
     from tests.selection_fixtures import c5_selection_input  # input generator, shared with the tests
@@ -285,6 +293,7 @@ def op_rows(capi, dev):
         rows.append(("softmax_4x400x400", "C5", n, lambda r, n=n: op_softmax(capi, dev, n, r)))
         rows.append(("maxpool_k5_256x20x20", "SPPF", n, lambda r, n=n: op_maxpool(capi, dev, n, r)))
         rows.append(("detect_decode_64+80x8400", "C4", n, lambda r, n=n: op_decode(capi, dev, n, r)))
+        rows.append(("permute_nchw_to_nhwc_64x80x80", "MAT", n, lambda r, n=n: op_permute(capi, dev, n, r)))
     for layout in ("contiguous", "transposed"):
         rows.append((f"detection_select_{layout}", "C5", 1, lambda r, l=layout: op_select(capi, dev, l)))
     return rows

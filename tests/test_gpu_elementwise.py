@@ -255,3 +255,28 @@ def test_errors_are_reported(gpu):
         capi.binary(capi.ADD, a, b)
     with pytest.raises(capi.ThinError, match="float32/float16"):
         capi.unary(capi.SILU, torch.ones(4, device=gpu, dtype=torch.int64))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.int32, torch.bfloat16])
+def test_transpose_copy(gpu, dtype):
+    """Batched 2-D transposes take the tiled path: full and partial tiles,
+    aligned and misaligned rows, NCHW <-> NHWC permutes; bit-exact."""
+    from thintnpu_amd import capi
+    g = gen(5)
+    raw = torch.randint(-2 ** 31, 2 ** 31 - 1, (3, 130, 1040), generator=g, dtype=torch.int64).to(torch.int32)
+    base = raw.view(dtype) if dtype.itemsize == 4 else raw.view(torch.int16).view(dtype)[..., :1040]
+    for shape in ((2, 64, 6400), (1, 130, 257), (3, 17, 1000), (1, 64, 64), (2, 100, 16)):
+        b, m, n = shape
+        x = base[:b, :m, :n]
+        for offset in (0, 1):
+            src = x[..., offset:]
+            got = torch.empty(src.transpose(1, 2).shape, dtype=dtype, device=gpu)
+            capi.copy(src.to(gpu).transpose(1, 2) if offset == 0 else x.to(gpu)[..., offset:].transpose(1, 2), got)
+            assert torch.equal(got.cpu().view(torch.uint8), src.transpose(1, 2).contiguous().view(torch.uint8))
+    x = torch.randn(2, 64, 20, 20, generator=g).to(dtype) if dtype.is_floating_point else \
+        torch.randint(-1000, 1000, (2, 64, 20, 20), generator=g).to(dtype)
+    for perm in ((0, 2, 3, 1), (0, 3, 1, 2)):
+        src = x.permute(*perm)
+        got = torch.empty(src.shape, dtype=dtype, device=gpu)
+        capi.copy(x.to(gpu).permute(*perm), got)
+        assert torch.equal(got.cpu().view(torch.uint8), src.contiguous().view(torch.uint8))

@@ -743,6 +743,117 @@ uint64_t fill_bits(int32_t dtype, double value, int64_t ivalue) {
   return 0;
 }
 
+// ------------------------------------------------------------ transpose
+// Batched 2-D transpose copy: dst[b][p][m] = src[b][m][p] where src rows run
+// along p (unit stride) and dst rows along m (unit stride) -- the layout of
+// x.permute(...).contiguous() for an NCHW <-> NHWC change.  A block moves a
+// 64 x 64 tile: 16-byte loads along src rows into LDS (rows padded by one
+// 4-byte word so that column reads hit distinct banks), then 16-byte stores
+// along dst rows.  Tile edges and unaligned rows take per-element accesses.
+constexpr uint32_t kTile = 64;
+
+struct TransposePlan {
+  const char* src;
+  char* dst;
+  uint32_t M, P, B;          // dst-inner extent, src-inner extent, batches
+  int64_t s_m, s_b;          // src strides (elements) of m and b; p stride is 1
+  int64_t d_p, d_b;          // dst strides (elements) of p and b; m stride is 1
+  uint32_t tiles_m, tiles_p;
+  uint32_t vec_src, vec_dst; // 16-byte rows possible (alignment checked on the host)
+};
+
+template <typename T, bool NT>
+__global__ __launch_bounds__(kThreads) void transpose_kernel(TransposePlan p) {
+  constexpr uint32_t V = 16 / sizeof(T);
+  constexpr uint32_t kRow = kTile + 4 / sizeof(T);  // padded LDS row, in elements
+  __shared__ __attribute__((aligned(16))) T tile[kTile * kRow];
+  const uint32_t per_b = p.tiles_m * p.tiles_p;
+  const uint32_t b = blockIdx.x / per_b, rest = blockIdx.x - b * per_b;
+  const uint32_t tm = rest / p.tiles_p, tp = rest - tm * p.tiles_p;
+  const uint32_t m0 = tm * kTile, p0 = tp * kTile;
+  const T* src = reinterpret_cast<const T*>(p.src) + b * p.s_b;
+  T* dst = reinterpret_cast<T*>(p.dst) + b * p.d_b;
+  const bool full = m0 + kTile <= p.M && p0 + kTile <= p.P;
+  // load: tile row r = m0 + r, columns p0 .. p0+63
+  for (uint32_t i = threadIdx.x; i < kTile * kTile / V; i += kThreads) {
+    const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+    const T* row = src + (int64_t)(m0 + r) * p.s_m + p0 + cv;
+    if (full && p.vec_src) {
+      const VecT<T, V> w = load16<NT, VecT<T, V>>(row);
+#pragma unroll
+      for (uint32_t j = 0; j < V; ++j) tile[r * kRow + cv + j] = w.v[j];
+    } else {
+#pragma unroll
+      for (uint32_t j = 0; j < V; ++j)
+        if (m0 + r < p.M && p0 + cv + j < p.P) tile[r * kRow + cv + j] = row[j];
+    }
+  }
+  __syncthreads();
+  // store: dst row p0 + q, columns m0 .. m0+63
+  for (uint32_t i = threadIdx.x; i < kTile * kTile / V; i += kThreads) {
+    const uint32_t q = i / (kTile / V), cm = (i % (kTile / V)) * V;
+    T* row = dst + (int64_t)(p0 + q) * p.d_p + m0 + cm;
+    VecT<T, V> w;
+#pragma unroll
+    for (uint32_t j = 0; j < V; ++j) w.v[j] = tile[(cm + j) * kRow + q];
+    if (full && p.vec_dst) {
+      store16<NT>(row, w);
+    } else {
+#pragma unroll
+      for (uint32_t j = 0; j < V; ++j)
+        if (p0 + q < p.P && m0 + cm + j < p.M) row[j] = w.v[j];
+    }
+  }
+}
+
+// Launches the tiled transpose when dst <- src is a batched 2-D transpose of
+// 2- or 4-byte elements; returns false (nothing launched) otherwise.
+bool try_transpose(const thin_desc* src, const thin_desc* dst, hipStream_t stream) {
+  const int esz = dtype_size(dst->dtype);
+  if (esz != 2 && esz != 4) return false;
+  const thin_desc* ops[2] = {dst, src};
+  Coalesced c = coalesce(ops, 2);
+  if (c.nd < 2 || c.nd > 3) return false;
+  const int in = c.nd - 1;                       // innermost dim: dst-contiguous
+  if (c.stride[0][in] != 1 || c.stride[1][in] == 1) return false;
+  int pd = -1;
+  for (int d = 0; d < in; ++d)
+    if (c.stride[1][d] == 1) pd = d;
+  if (pd < 0) return false;
+  const int bd = c.nd == 3 ? (pd == 0 ? 1 : 0) : -1;
+  const int64_t M = c.size[in], P = c.size[pd], B = bd >= 0 ? c.size[bd] : 1;
+  if (M < 16 || P < 16) return false;            // thin slabs: the vector map path is as good
+  TransposePlan t;
+  t.src = static_cast<const char*>(src->data);
+  t.dst = static_cast<char*>(dst->data);
+  t.M = (uint32_t)M;
+  t.P = (uint32_t)P;
+  t.B = (uint32_t)B;
+  t.s_m = c.stride[1][in];
+  t.d_p = c.stride[0][pd];
+  t.s_b = bd >= 0 ? c.stride[1][bd] : 0;
+  t.d_b = bd >= 0 ? c.stride[0][bd] : 0;
+  t.tiles_m = (uint32_t)((M + kTile - 1) / kTile);
+  t.tiles_p = (uint32_t)((P + kTile - 1) / kTile);
+  const uint64_t blocks = (uint64_t)B * t.tiles_m * t.tiles_p;
+  if (M >= (1ll << 31) || P >= (1ll << 31) || blocks >= (1ull << 31)) return false;
+  auto a16 = [](const void* q, int64_t stride, int e) {
+    return reinterpret_cast<uintptr_t>(q) % 16 == 0 && (stride * e) % 16 == 0;
+  };
+  t.vec_src = a16(src->data, t.s_m, esz) && (t.s_b * esz) % 16 == 0;
+  t.vec_dst = a16(dst->data, t.d_p, esz) && (t.d_b * esz) % 16 == 0;
+  const bool nt = (int64_t)B * M * P * esz >= kStreamingStoreBytes;
+  if (esz == 2 && nt)
+    hipLaunchKernelGGL((transpose_kernel<uint16_t, true>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+  else if (esz == 2)
+    hipLaunchKernelGGL((transpose_kernel<uint16_t, false>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+  else if (nt)
+    hipLaunchKernelGGL((transpose_kernel<uint32_t, true>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+  else
+    hipLaunchKernelGGL((transpose_kernel<uint32_t, false>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+  return true;
+}
+
 // Raw bit copy used by the copy/cat/materialize paths.
 thin_status copy_bits(const thin_desc* src, const thin_desc* dst, hipStream_t stream) {
   const thin_desc* ins[1] = {src};
@@ -860,6 +971,11 @@ extern "C" thin_status thin_copy(const thin_desc* src, const thin_desc* dst, hip
   THIN_REQUIRE(same_sizes(src, dst), THIN_ERR_INVALID, "copy requires matching sizes");
   THIN_REQUIRE(dtype_size(src->dtype) == dtype_size(dst->dtype) && src->dtype == dst->dtype,
                THIN_ERR_INVALID, "copy requires matching dtypes");
+  if (numel(dst) == 0) return THIN_OK;
+  if (try_transpose(src, dst, stream)) {
+    THIN_LAUNCH_CHECK("transpose");
+    return THIN_OK;
+  }
   return copy_bits(src, dst, stream);
 }
 
