@@ -132,6 +132,12 @@ size_t round_size(size_t n) {
   return (n + ((size_t)2 << 20) - 1) & ~(((size_t)2 << 20) - 1);
 }
 
+// Caching allocator.  A freed block returns to the free list of the stream it
+// was allocated on and is reused only by later allocations on that stream, so
+// reuse is ordered after every kernel that stream enqueued with it.  A tensor
+// whose memory another host thread's stream still reads must be synchronized
+// by the caller before it is released (the reference synchronizes after every
+// op; THIN_SYNC=1 restores that).
 class Pool {
  public:
   void* alloc(size_t n) {
@@ -192,6 +198,7 @@ class Pool {
   }
 
   void empty_cache() {
+    if (capturing()) return;  // no device-wide synchronize inside a capture
     std::lock_guard<std::mutex> lock(mutex_);
     release_cached_locked();
   }
@@ -267,7 +274,9 @@ struct Guard final : c10::impl::DeviceGuardImplInterface {
     return hipGetDeviceCount(&n) == hipSuccess && n > 0 ? 1 : 0;
   }
   void synchronizeStream(const c10::Stream&) const override { sync(); }
-  void synchronizeDevice(c10::DeviceIndex) const override { sync(); }
+  void synchronizeDevice(c10::DeviceIndex) const override {
+    if (!capturing()) hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  }
 };
 
 // ------------------------------------------------------------------ factories
