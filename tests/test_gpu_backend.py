@@ -446,3 +446,25 @@ def test_materialize_cases(npu, dtype):
         assert bits_equal(raw.to(npu).transpose(1, 2).contiguous().cpu(), raw.transpose(1, 2).contiguous())
         slices = [raw[..., :2].contiguous(), raw[..., 2:4].contiguous(), raw[..., 4:16].contiguous()]
         assert bits_equal(torch.cat([s.to(npu) for s in slices], -1).cpu(), torch.cat(slices, -1))
+
+
+def test_decode_constants(npu):
+    """verify_decode.py restated: arange / full / stack / broadcast add /
+    scalar mul and div / unbind / _local_scalar_dense on npu (decode.cpp:6-34)."""
+    with torch.inference_mode():
+        cases = {
+            "arange": lambda d: torch.arange(80, device=d, dtype=torch.float32),
+            "arange_step": lambda d: torch.arange(-2, 10, 0.5, device=d, dtype=torch.float32),
+            "full": lambda d: torch.full((8400, 1), 8.0, device=d),
+            "stack": lambda d: torch.stack((torch.arange(80, device=d, dtype=torch.float32),
+                                            torch.arange(80, device=d, dtype=torch.float32)), dim=-1),
+            "broadcast_add": lambda d: torch.arange(80, device=d, dtype=torch.float32).view(1, 80)
+            + torch.full((2, 1), 0.5, device=d),
+            "scalar_mul": lambda d: torch.arange(80, device=d, dtype=torch.float32) * 8,
+            "scalar_div": lambda d: torch.arange(80, device=d, dtype=torch.float32) / 2,
+        }
+        for name, call in cases.items():
+            torch.testing.assert_close(call("npu").cpu(), call("cpu"), rtol=0, atol=0, msg=name)
+        x = torch.arange(12, device="npu", dtype=torch.float32).view(3, 4)
+        torch.testing.assert_close(torch.stack(torch.unbind(x)).cpu(), torch.arange(12, dtype=torch.float32).view(3, 4))
+        assert torch.full((), 8.0, device="npu").item() == 8.0
