@@ -11,8 +11,9 @@ in HBM and buffer sets rotated (> 512 MB) so the 256 MB Infinity Cache cannot
 serve them.
 
 Also reported (``ops``): per-op / per-chain µs and GB/s at N=1 (cache-resident
-and rotated) and N=32 for every op built, the roofline of the dominant kernel
-and the PyTorch CPU op sequence timed on the host cores (``cpu_baseline``).
+and rotated) and N=32 for every op built, each beside the reference's CPU path
+(the stock PyTorch CPU op sequence) timed on the host cores, the roofline of
+the dominant kernel, and the CPU path of the step itself (``cpu_baseline``).
 Only rank 0 prints: one JSON line on stdout; progress goes to stderr.
 """
 from __future__ import annotations
@@ -301,6 +302,76 @@ def op_rows(capi, dev):
 
 # ------------------------------------------------------------------ CPU baseline
 
+def cpu_op(name, n):
+    """(callable, algorithmic bytes) running the reference's CPU path of one op
+    row -- the stock PyTorch CPU op sequence its tests compare against -- on
+    seeded CPU tensors of the row's shape; None for rows without one."""
+    import torch.nn.functional as F
+    g = gen(7)
+    h16 = lambda *shape: torch.randn(shape, generator=g).half()  # noqa: E731
+    if name == "silu_add":
+        x, y = h16(n, 4, 160, 160, 16), h16(n, 4, 160, 160, 16)
+        return (lambda: y + F.silu(x)), n * 4 * 160 * 160 * 16 * 2 * 3
+    if name == "pack_nc1hwc0":
+        x = h16(n, 64, 160, 160)
+        return (lambda: x.view(n, 4, 16, 160, 160).permute(0, 1, 3, 4, 2).contiguous()), x.numel() * 4
+    if name.startswith("affine_silu"):
+        c, h, w = (int(v) for v in name.rsplit("_", 1)[1].split("x"))
+        c1 = c // 16
+        x, sc, b = h16(n, c1, h, w, 16), h16(1, c1, 1, 1, 16).abs() + 0.5, h16(1, c1, 1, 1, 16) * 0.1
+        if "narrowed" in name:
+            x, sc, b = x[:, c1 // 2:], sc[:, c1 // 2:], b[:, c1 // 2:]
+        return (lambda: F.silu(torch.add(torch.mul(x, sc), b))), x.numel() * 4
+    if name == "cat_c2f_4x64":
+        parent, c, d = h16(n, 8, 80, 80, 16), h16(n, 4, 80, 80, 16), h16(n, 4, 80, 80, 16)
+        return (lambda: torch.cat([parent[:, :4], parent[:, 4:], c, d], 1)), n * 16 * 80 * 80 * 16 * 4
+    if name == "upsample2x_256x40x40":
+        x = h16(n, 16, 40, 40, 16)
+        return (lambda: x.repeat_interleave(2, 2).repeat_interleave(2, 3)), x.numel() * 2 * 5
+    if name == "upsample_cat_256+128":
+        x, y = h16(n, 16, 40, 40, 16), h16(n, 8, 80, 80, 16)
+        return (lambda: torch.cat((x.repeat_interleave(2, 2).repeat_interleave(2, 3), y), 1)), \
+            (x.numel() + y.numel() + n * 24 * 80 * 80 * 16) * 2
+    if name == "dfl_expect_64x8400":
+        x = h16(n, 64, 8400) * 3
+        w = torch.arange(16, dtype=torch.float32).view(1, 1, 16, 1)
+        return (lambda: (torch.softmax(x.float().view(n, 4, 16, 8400), 2) * w).sum(2).half()), \
+            n * (64 + 4) * 8400 * 2
+    if name == "sigmoid_80x8400":
+        x = h16(n, 80, 8400)
+        return (lambda: torch.sigmoid(x)), x.numel() * 4
+    if name == "softmax_4x400x400":
+        x = h16(n, 4, 400, 400)
+        return (lambda: torch.softmax(x, -1)), x.numel() * 4
+    if name == "maxpool_k5_256x20x20":
+        x = h16(n, 256, 20, 20)
+        return (lambda: F.max_pool2d(x.float(), 5, 1, 2).half()), x.numel() * 4
+    if name == "detect_decode_64+80x8400":
+        from oracle import detect as dt  # the CPU decode sequence, timed
+        b, sc = h16(n, 64, 8400) * 3, h16(n, 80, 8400)
+        shapes, strides = [(80, 80), (40, 40), (20, 20)], [8.0, 16.0, 32.0]
+        return (lambda: dt.detect_decode(b, sc, shapes, strides)), n * 8400 * 2 * (64 + 80 + 84)
+    if name == "permute_nchw_to_nhwc_64x80x80":
+        x = h16(n, 64, 80, 80)
+        return (lambda: x.permute(0, 2, 3, 1).contiguous()), x.numel() * 4
+    if name.startswith("detection_select"):
+        from oracle import selection as sel  # the stable CPU selection, timed
+        from tests.selection_fixtures import c5_selection_input
+        x = c5_selection_input()
+        return (lambda: sel.select(x, 300, False)), 8400 * 84 * 2 + 300 * 6 * 4
+    return None
+
+
+def time_cpu(fn, budget_s=0.4, max_samples=10):
+    fn()
+    samples, t_end = [], time.perf_counter() + budget_s
+    while len(samples) < 2 or (len(samples) < max_samples and time.perf_counter() < t_end):
+        t0 = time.perf_counter_ns()
+        fn()
+        samples.append((time.perf_counter_ns() - t0) / 1e9)
+    return statistics.median(samples)
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's CPU op sequence F.silu(torch.add(torch.mul(x, s), b)) in
     fp16 (restated by the oracle) over the same step as the GPU figure -- N=32,
@@ -440,15 +511,28 @@ def main():
     if not args.no_ops:
         for name, cfg, nn, factory in op_rows(capi, dev):
             modes = (False,) if name.startswith("detection_select") else ((False, True) if nn == 1 else (True,))
+            cpu_row = None
+            if not args.no_cpu:
+                made = cpu_op(name, nn)
+                if made is not None:
+                    fn, cpu_bytes = made
+                    ct = time_cpu(fn)
+                    cpu_row = {"cpu_us": round(ct * 1e6, 1), "cpu_GB/s": round(cpu_bytes / ct / 1e9, 2),
+                               "cpu_threads": torch.get_num_threads()}
+                    del fn
             for rotate in modes:
                 launch, sets, algo = factory(rotate)
                 t = time_launches(launch, sets, args.iters)
                 gbs = algo / t / 1e9
-                ops.append({"op": name, "cfg": cfg, "N": nn, "us": round(t * 1e6, 3),
-                            "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
-                            "bytes": algo, "cache": "rotated" if rotate else "resident"})
+                row = {"op": name, "cfg": cfg, "N": nn, "us": round(t * 1e6, 3),
+                       "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+                       "bytes": algo, "cache": "rotated" if rotate else "resident"}
+                if cpu_row:
+                    row.update(cpu_row)
+                ops.append(row)
                 log(f"{cfg} {name:32s} N={nn:2d} {'rot' if rotate else 'res'} "
-                    f"{t * 1e6:9.2f} us {gbs:8.1f} GB/s")
+                    f"{t * 1e6:9.2f} us {gbs:8.1f} GB/s" +
+                    (f"   cpu {cpu_row['cpu_us']:10.1f} us" if cpu_row else ""))
                 del sets
                 torch.cuda.empty_cache()
 
