@@ -182,14 +182,12 @@ __device__ __forceinline__ W load16(const void* src) {
   return __builtin_bit_cast(W, bits);
 }
 
-// Outputs of at least this many bytes are written with streaming
+// Outputs of at least kStreamingBytes are written with streaming
 // (non-temporal) stores, and inputs read once in full at that size are read
-// with streaming loads; smaller ones stay cached so that producer and consumer
-// kernels meet in L2 / MALL.  Operands re-read across the grid (broadcast
+// with streaming loads.  Operands re-read across the grid (broadcast
 // scale/bias) always use cached loads.  On gfx950, 256-thread blocks with two
 // 16-byte vectors per thread and one tile per block measured best for every
 // kernel here (1024-thread blocks and 4-8 vectors per thread were slower).
-constexpr int64_t kStreamingStoreBytes = (int64_t)16 << 20;
 
 // Unit offsets for the vector kernel; ND == 1 means every operand is flat
 // (one coalesced dim), so the unit index is the element offset times stride.
@@ -485,7 +483,7 @@ bool try_affine_flat(const thin_desc* x, const thin_desc* sc, const thin_desc* b
   p.b_c1 = (uint32_t)(b->strides[1] / 8);
   p.c1 = (uint32_t)c1;
   const uint32_t grid = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
-  const bool nt = total * 16 >= kStreamingStoreBytes;
+  const bool nt = total * 16 >= kStreamingBytes;
   if (nt) hipLaunchKernelGGL((affine_silu_flat_kernel<true, true>), dim3(grid), dim3(kThreads), 0, stream, p);
   else hipLaunchKernelGGL((affine_silu_flat_kernel<false, false>), dim3(grid), dim3(kThreads), 0, stream, p);
   return true;
@@ -522,7 +520,7 @@ bool try_affine_blocked(const thin_desc* x, const thin_desc* sc, const thin_desc
   p.planes = (uint32_t)planes;
   p.plane_vecs = (uint32_t)plane_vecs;
   const uint32_t gy = planes < 65535 ? (uint32_t)planes : 65535u;
-  const bool nt = planes * plane_vecs * 16 >= kStreamingStoreBytes;
+  const bool nt = planes * plane_vecs * 16 >= kStreamingBytes;
   if (plane_vecs >= 1024) {
     uint32_t gx = (uint32_t)((plane_vecs + kThreads * 2 - 1) / (kThreads * 2));
     if (nt) hipLaunchKernelGGL((affine_silu_blocked_kernel<2, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
@@ -650,7 +648,7 @@ thin_status launch_map(const thin_desc* out, const thin_desc* const* ins, float 
     } else {
       p.units = (uint32_t)elems;
     }
-    const bool nt = elems * (int64_t)sizeof(T) >= kStreamingStoreBytes;
+    const bool nt = elems * (int64_t)sizeof(T) >= kStreamingBytes;
     if (nd == 1) launch_plan<T, NIN, 1, Op>(p, vec, nt, stream);
     else if (nd <= 2) launch_plan<T, NIN, 2, Op>(p, vec, nt, stream);
     else if (nd <= 4) launch_plan<T, NIN, 4, Op>(p, vec, nt, stream);
@@ -842,7 +840,7 @@ bool try_transpose(const thin_desc* src, const thin_desc* dst, hipStream_t strea
   };
   t.vec_src = a16(src->data, t.s_m, esz) && (t.s_b * esz) % 16 == 0;
   t.vec_dst = a16(dst->data, t.d_p, esz) && (t.d_b * esz) % 16 == 0;
-  const bool nt = (int64_t)B * M * P * esz >= kStreamingStoreBytes;
+  const bool nt = (int64_t)B * M * P * esz >= kStreamingBytes;
   if (esz == 2 && nt)
     hipLaunchKernelGGL((transpose_kernel<uint16_t, true>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
   else if (esz == 2)

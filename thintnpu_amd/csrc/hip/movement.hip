@@ -18,7 +18,6 @@ thin_status copy_bits(const thin_desc* src, const thin_desc* dst, hipStream_t st
 namespace {
 
 constexpr uint32_t kThreads = 256;
-constexpr int64_t kStreamingStoreBytes = (int64_t)16 << 20;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -37,8 +36,8 @@ __device__ __forceinline__ u32x4 ld16s(const void* src) {
   return *reinterpret_cast<const u32x4*>(src);
 }
 
-// Large outputs (>= kStreamingStoreBytes) are written with streaming stores;
-// loads stay cached (see the launch-shape note in elementwise.hip).
+// Launches whose output reaches kStreamingBytes use streaming stores, and
+// streaming loads for inputs read once (cat, plane copies, pack).
 constexpr uint32_t kStreamThreads = 256;
 
 // ============================================================ cat
@@ -291,7 +290,7 @@ thin_status launch_planes(const thin_desc* ins, const int32_t* up, int count, co
   p.units = (uint32_t)units;
   p.div_plane = FastDiv::make(p.plane_vecs);
   p.div_c1 = FastDiv::make(p.out_c1_total);
-  if ((int64_t)units * 16 >= kStreamingStoreBytes) {
+  if ((int64_t)units * 16 >= kStreamingBytes) {
     const uint32_t grid = grid_for(units, kStreamThreads, 2, 256u * 64u);
     hipLaunchKernelGGL((plane_kernel<2, true, kStreamThreads>), dim3(grid), dim3(kStreamThreads), 0, stream, p);
   } else {
@@ -773,7 +772,7 @@ thin_status repack(const thin_desc* nchw, const thin_desc* blocked, bool to_bloc
                  ? 1u : 0u;
   const uint64_t blocks = (uint64_t)n * c1 * p.tiles;
   THIN_REQUIRE(blocks < (1ull << 31), THIN_ERR_UNSUPPORTED, "repack: too many tiles");
-  const bool nt = n * c1 * h * w * 32 >= kStreamingStoreBytes;
+  const bool nt = n * c1 * h * w * 32 >= kStreamingBytes;
   if (to_blocked && nt)
     hipLaunchKernelGGL(pack_kernel<true>, dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
   else if (to_blocked)
@@ -816,7 +815,7 @@ extern "C" thin_status thin_cat(const thin_desc* inputs, int32_t n, int32_t dim,
   const bool out_dense = is_contiguous(out);
   int64_t inner = 1;
   for (int d = dim + 1; d < out->rank; ++d) inner *= out->sizes[d];
-  const bool nt = numel(out) * esize >= kStreamingStoreBytes;
+  const bool nt = numel(out) * esize >= kStreamingBytes;
   const bool out_vec = aligned16(out->data) && (out->sizes[dim] * inner * esize) % 16 == 0;
   const thin_desc* vec_in[kCatPerLaunch];
   int64_t vec_col[kCatPerLaunch];
@@ -950,7 +949,7 @@ extern "C" thin_status thin_upsample2x_nchw(const thin_desc* x, const thin_desc*
   p.div_row_vecs = FastDiv::make(p.row_vecs);
   p.div_oh = FastDiv::make(p.oh);
   p.div_c = FastDiv::make(p.c);
-  const bool nt = numel(y) * esize >= kStreamingStoreBytes;
+  const bool nt = numel(y) * esize >= kStreamingBytes;
   const uint32_t grid = grid_for(rows * p.row_vecs, kThreads, 1, 256u * 16u);
   if (esize == 2) {
     if (nt) hipLaunchKernelGGL((nchw_up_kernel<uint16_t, true>), dim3(grid), dim3(kThreads), 0, stream, p);

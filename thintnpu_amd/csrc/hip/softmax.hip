@@ -409,9 +409,8 @@ void column_space(const thin_desc* x, const thin_desc* out, int dim, SoftmaxPlan
   }
 }
 
-// Streaming (non-temporal) loads and stores for launches moving at least this
-// many bytes; smaller ones stay cached for their producer and consumer.
-constexpr int64_t kStreamingBytes = (int64_t)16 << 20;
+// Streaming (non-temporal) loads and stores for launches moving at least
+// kStreamingBytes.
 
 // Lanes per row G and chunks per lane KPT for a row of `chunks` (<= 512).
 template <typename TI, typename TO, bool VEC, bool FAST, bool NT>
