@@ -362,14 +362,18 @@ def cpu_op(name, n):
     return None
 
 
-def time_cpu(fn, budget_s=0.4, max_samples=10):
-    fn()
+def time_cpu(fn, warmup=3, min_samples=20, floor_samples=5, budget_s=1.0):
+    """(median seconds, sample count) of fn(): `warmup` untimed calls, then
+    `min_samples` timed ones -- cut to `floor_samples` when single calls are so
+    slow that the samples would run past `budget_s`."""
+    for _ in range(warmup):
+        fn()
     samples, t_end = [], time.perf_counter() + budget_s
-    while len(samples) < 2 or (len(samples) < max_samples and time.perf_counter() < t_end):
+    while len(samples) < min_samples and (len(samples) < floor_samples or time.perf_counter() < t_end):
         t0 = time.perf_counter_ns()
         fn()
         samples.append((time.perf_counter_ns() - t0) / 1e9)
-    return statistics.median(samples)
+    return statistics.median(samples), len(samples)
 
 
 def cpu_baseline(budget_s=12.0):
@@ -516,9 +520,17 @@ def main():
                 made = cpu_op(name, nn)
                 if made is not None:
                     fn, cpu_bytes = made
-                    ct = time_cpu(fn)
+                    threads = torch.get_num_threads()
+                    ct, ns = time_cpu(fn)
+                    torch.set_num_threads(1)  # the reference tests' thread count
+                    try:
+                        ct1, ns1 = time_cpu(fn)
+                    finally:
+                        torch.set_num_threads(threads)
                     cpu_row = {"cpu_us": round(ct * 1e6, 1), "cpu_GB/s": round(cpu_bytes / ct / 1e9, 2),
-                               "cpu_threads": torch.get_num_threads()}
+                               "cpu_threads": threads, "cpu_samples": ns,
+                               "cpu1_us": round(ct1 * 1e6, 1), "cpu1_GB/s": round(cpu_bytes / ct1 / 1e9, 2),
+                               "cpu1_samples": ns1}
                     del fn
             for rotate in modes:
                 launch, sets, algo = factory(rotate)
@@ -532,7 +544,8 @@ def main():
                 ops.append(row)
                 log(f"{cfg} {name:32s} N={nn:2d} {'rot' if rotate else 'res'} "
                     f"{t * 1e6:9.2f} us {gbs:8.1f} GB/s" +
-                    (f"   cpu {cpu_row['cpu_us']:10.1f} us" if cpu_row else ""))
+                    (f"   cpu {cpu_row['cpu_us']:10.1f} us  1 thread {cpu_row['cpu1_us']:10.1f} us"
+                     if cpu_row else ""))
                 del sets
                 torch.cuda.empty_cache()
 

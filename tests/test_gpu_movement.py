@@ -206,6 +206,54 @@ def test_maxpool_nc1hwc0(gpu, n):
         check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"specials k{k}")
 
 
+def pool_specials_packed(x, zero, seed):
+    """Infinities, NaNs of both signs, subnormals of both signs and zeros of
+    one sign (`zero` = 0.0, -0.0 or None) written into x (fp16): tiles the
+    packed IEEE-maximum path takes, since only a +0/-0 tie separates it from
+    the first-maximum rule."""
+    x = x.clone()
+    bits = x.view(-1).view(torch.int16)
+    n = bits.numel()
+    g = gen(seed)
+    at = lambda count: torch.randint(0, n, (count,), generator=g)  # noqa: E731
+    sub = torch.randint(1, 0x400, (n // 50,), generator=g, dtype=torch.int32)
+    sub = torch.where(torch.rand(n // 50, generator=g) < 0.5, sub, sub | 0x8000)
+    bits[at(n // 50)] = (sub - ((sub >> 15) << 16)).to(torch.int16)  # subnormals, both signs
+    for pattern, count in ((0x7C00, 3), (0xFC00 - 0x10000, 5), (0x7E00, 3), (0xFE01 - 0x10000, 3), (0x7C01, 2)):
+        bits[at(count)] = pattern  # +inf, -inf, +qNaN, -NaN, +sNaN payload
+    if zero is not None:
+        x.view(-1)[at(n // 20)] = zero
+    return x
+
+
+@pytest.mark.parametrize("zero", [None, 0.0, -0.0])
+def test_maxpool_packed_specials(gpu, zero):
+    """fp16 NC1HWC0 tiles without a +0/-0 mix: NaN propagation, infinities,
+    subnormals and single-signed zeros through the packed maximum."""
+    from thintnpu_amd import capi
+    x = pool_specials_packed(to_blocked(normal16((2, 64, 20, 20), 31)), zero, 41)
+    for k in (1, 3, 5, 7, 15):
+        check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"packed zero={zero} k{k}")
+    # subnormal-only windows: maxima between subnormals are kept exactly
+    tiny = to_blocked(normal16((1, 32, 12, 12), 5)) * 1e-6
+    tiny[tiny == 0] = 2.0 ** -24
+    assert (tiny.abs() < 6.1e-5).all() and (tiny != 0).all()
+    check_pool(capi.maxpool_nc1hwc0(tiny.to(gpu), 5).cpu(), mv.maxpool_blocked(tiny, 5), "subnormal planes")
+
+
+def test_maxpool_mixed_blocks(gpu):
+    """One plane holds +0/-0 ties (first-maximum selects) while the rest of the
+    launch takes the packed path."""
+    from thintnpu_amd import capi
+    x = to_blocked(normal16((2, 64, 20, 20), 12))
+    x[1, 2] = pool_specials(x[1, 2:3])[0]
+    x[0, 1] = -x[0, 1].abs()
+    x[0, 1, ::3, ::2] = -0.0
+    x[0, 1, 1::4, 1::3] = 0.0
+    for k in (3, 5, 9):
+        check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"mixed k{k}")
+
+
 def test_maxpool_views(gpu):
     from thintnpu_amd import capi
     x = to_blocked(normal16((2, 64, 12, 10), 8))

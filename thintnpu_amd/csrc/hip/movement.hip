@@ -9,6 +9,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 #include <string.h>
 
@@ -414,6 +415,7 @@ struct PoolPlan {
   uint32_t units;         // planes * chunks * w * parts
   FastDiv div_parts, div_w, div_chunks, div_c;
   FastDiv div_row;        // w * parts (LDS form)
+  FastDiv div_prow;       // (w + k - 1) * parts: LDS input rows padded with k/2 -inf pixels each side
 };
 
 template <typename T, int V>
@@ -476,19 +478,33 @@ __global__ __launch_bounds__(kThreads) void maxpool_kernel(PoolPlan p) {
 
 // LDS-tiled form: a block takes one plane band of `rows` output rows.  The
 // band's input rows plus the 2R halo rows are read once (coalesced) into LDS,
-// horizontal maxima go to a second LDS buffer, vertical maxima to HBM -- one
-// global round trip per block instead of one per output row.
+// with R -inf pixels padding each row on both sides (so no tap needs a bounds
+// check), horizontal maxima go to a second LDS buffer, vertical maxima to HBM
+// -- one global round trip per block instead of one per output row.
+//
+// fp16 pixel vectors take a packed path: the IEEE-754 2019 maximum
+// (v_pk_maximum3_f16, two taps per instruction) propagates NaN and orders
+// -0 < +0, so it selects the same bits as the first-maximum rule except where
+// a window's maximum is a +0/-0 tie.  A block whose tile holds zeros of both
+// signs therefore keeps the first-maximum selects; other blocks take the
+// packed path.
 template <typename T, int V, int K>
 __global__ __launch_bounds__(kThreads) void maxpool_tile_kernel(PoolPlan p, uint32_t bands) {
   constexpr int R = K / 2;
+  constexpr bool kPacked = std::is_same<T, _Float16>::value && V == 8;
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
   extern __shared__ __attribute__((aligned(16))) char pool_lds[];
+  __shared__ uint32_t wave_zero_signs[kThreads / 64];
   typedef PoolVec<T, V> PV;
   const uint32_t plane = blockIdx.x / bands, band = blockIdx.x - plane * bands;
   const uint32_t n = p.div_c.div(plane), c = plane - n * p.c;
   const int y0 = (int)(band * p.rows);
   const int tile_rows = (int)p.rows + 2 * R;
   const uint32_t row_vecs = p.w * p.parts;
-  const uint32_t tile = (uint32_t)tile_rows * row_vecs;
+  const uint32_t prow = p.div_prow.d;
+  const uint32_t tile = (uint32_t)tile_rows * prow;
+  const uint32_t htile = (uint32_t)tile_rows * row_vecs;
   PV* in = reinterpret_cast<PV*>(pool_lds);
   PV* hm = in + tile;
   PV ninf;
@@ -496,6 +512,9 @@ __global__ __launch_bounds__(kThreads) void maxpool_tile_kernel(PoolPlan p, uint
   for (int j = 0; j < V; ++j) ninf.e[j] = (T)(-__builtin_inff());
   const T* xp = reinterpret_cast<const T*>(p.x) + n * p.xs[0] + c * p.xs[1];
   const uint32_t pshift = p.parts == 2 ? 1u : 0u;
+  // per-thread minima of the loaded bits and of the bits with the sign
+  // flipped: a zero lane means the tile holds a +0 (resp. a -0)
+  u16x8 min_pos = (u16x8)(uint16_t)0xffff, min_neg = (u16x8)(uint16_t)0xffff;
   // four loads in flight per thread before their LDS writes
   constexpr int U = 4;
   for (uint32_t i0 = threadIdx.x; i0 < tile; i0 += U * kThreads) {
@@ -505,27 +524,53 @@ __global__ __launch_bounds__(kThreads) void maxpool_tile_kernel(PoolPlan p, uint
       const uint32_t i = i0 + u * kThreads;
       v[u] = ninf;
       if (i < tile) {
-        const uint32_t rr = p.div_row.div(i), k = i - rr * row_vecs;
-        const uint32_t x = k >> pshift, part = k & pshift;
+        const uint32_t rr = p.div_prow.div(i), k = i - rr * prow;
+        const int x = (int)(k >> pshift) - R;
+        const uint32_t part = k & pshift;
         const int yy = y0 - R + (int)rr;
-        if (yy >= 0 && yy < (int)p.h)
+        if (yy >= 0 && yy < (int)p.h && x >= 0 && x < (int)p.w) {
           v[u] = *reinterpret_cast<const PV*>(xp + (int64_t)yy * p.xs[2] + (int64_t)x * p.xs[3] + (int64_t)part * V);
+          if constexpr (kPacked) {
+            const u16x8 b = __builtin_bit_cast(u16x8, v[u]);
+            min_pos = __builtin_elementwise_min(min_pos, b);
+            min_neg = __builtin_elementwise_min(min_neg, b ^ (uint16_t)0x8000);
+          }
+        }
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (i0 + u * kThreads < tile) in[i0 + u * kThreads] = v[u];
   }
+  bool exact = !kPacked;
+  if constexpr (kPacked) {
+    const uint32_t has = (__ballot(__builtin_reduce_min(min_pos) == 0) != 0 ? 1u : 0u) |
+                         (__ballot(__builtin_reduce_min(min_neg) == 0) != 0 ? 2u : 0u);
+    if ((threadIdx.x & 63u) == 0) wave_zero_signs[threadIdx.x >> 6] = has;
+  }
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < tile; i += kThreads) {
+  if constexpr (kPacked) {
+    uint32_t has = 0;
+#pragma unroll
+    for (int wv = 0; wv < kThreads / 64; ++wv) has |= wave_zero_signs[wv];
+    exact = has == 3u;
+  }
+  for (uint32_t i = threadIdx.x; i < htile; i += kThreads) {
     const uint32_t rr = p.div_row.div(i), k = i - rr * row_vecs;
-    const uint32_t x = k >> pshift;
+    const uint32_t base = rr * prow + k;
+    if constexpr (kPacked) {
+      if (!exact) {
+        const h8* ih = reinterpret_cast<const h8*>(in);
+        h8 m = ih[base];
+#pragma unroll
+        for (int j = 1; j <= 2 * R; ++j) m = __builtin_elementwise_maximum(m, ih[base + j * (int)p.parts]);
+        reinterpret_cast<h8*>(hm)[i] = m;
+        continue;
+      }
+    }
     PV m = ninf;
 #pragma unroll
-    for (int dx = -R; dx <= R; ++dx) {
-      const int xx = (int)x + dx;
-      if (xx >= 0 && xx < (int)p.w) keep_max(m, in[i + dx * (int)p.parts]);
-    }
+    for (int j = 0; j <= 2 * R; ++j) keep_max(m, in[base + j * (int)p.parts]);
     hm[i] = m;
   }
   __syncthreads();
@@ -536,9 +581,21 @@ __global__ __launch_bounds__(kThreads) void maxpool_tile_kernel(PoolPlan p, uint
     const int y = y0 + (int)ry;
     if (y >= (int)p.h) break;
     const uint32_t x = k >> pshift, part = k & pshift;
-    PV m = ninf;
+    PV m;
+    if constexpr (kPacked) {
+      if (!exact) {
+        const h8* hh = reinterpret_cast<const h8*>(hm);
+        h8 mh = hh[ry * row_vecs + k];
 #pragma unroll
-    for (int dy = 0; dy <= 2 * R; ++dy) keep_max(m, hm[(ry + dy) * row_vecs + k]);
+        for (int dy = 1; dy <= 2 * R; ++dy) mh = __builtin_elementwise_maximum(mh, hh[(ry + dy) * row_vecs + k]);
+        m = __builtin_bit_cast(PV, mh);
+      }
+    }
+    if (exact) {
+      m = ninf;
+#pragma unroll
+      for (int dy = 0; dy <= 2 * R; ++dy) keep_max(m, hm[(ry + dy) * row_vecs + k]);
+    }
     *reinterpret_cast<PV*>(yp + (int64_t)y * p.ys[2] + (int64_t)x * p.ys[3] + (int64_t)part * V) = m;
   }
 }
@@ -549,11 +606,12 @@ template <typename T, int V>
 thin_status launch_pool(PoolPlan& p, uint32_t planes, int kernel, hipStream_t stream) {
   const int R = kernel / 2;
   const size_t row_bytes = (size_t)p.w * p.parts * sizeof(PoolVec<T, V>);
+  const size_t prow_bytes = (size_t)(p.w + 2 * R) * p.parts * sizeof(PoolVec<T, V>);
   const uint64_t plane_rows = (uint64_t)planes * p.h;
   // LDS form: band height for >= ~2048 blocks (several per CU to overlap the
   // load round trip of one band with the max passes of another), within the
-  // LDS budget (in + hm); halo rows are re-read from L2
-  const size_t max_tile_rows = kPoolLdsBytes / (2 * row_bytes);
+  // LDS budget (padded in + hm); halo rows are re-read from L2
+  const size_t max_tile_rows = kPoolLdsBytes / (prow_bytes + row_bytes);
   if (max_tile_rows > (size_t)(2 * R)) {
     uint32_t rows = (uint32_t)((plane_rows + 2047) / 2048);
     rows = std::max<uint32_t>(1u, std::min<uint32_t>(rows, p.h));
@@ -564,7 +622,8 @@ thin_status launch_pool(PoolPlan& p, uint32_t planes, int kernel, hipStream_t st
     p.rows = rows;
     p.div_c = FastDiv::make(p.c);
     p.div_row = FastDiv::make(p.w * p.parts);
-    const size_t lds = 2 * (size_t)(rows + 2 * R) * row_bytes;
+    p.div_prow = FastDiv::make((p.w + 2 * R) * p.parts);
+    const size_t lds = (size_t)(rows + 2 * R) * (prow_bytes + row_bytes);
     switch (kernel) {
 #define THIN_POOLT(KK)                                                                                       \
   case KK:                                                                                                    \
