@@ -88,3 +88,26 @@ def test_decode_npu_to_selection(gpu):
         for _ in range(3):
             assert bits_equal(graph.replay().cpu(), eager)
         graph.close()
+
+
+def test_offsets_beyond_4gib(gpu):
+    """Logits whose byte offsets pass 4 GiB take the 64-bit pointer loads; they
+    give the same bits as the 32-bit buffer-resource loads on a compact copy
+    (DFL and decode)."""
+    from thintnpu_amd import capi
+    a = 8400
+    shapes, strides = [(80, 80), (40, 40), (20, 20)], [8.0, 16.0, 32.0]
+    batch_stride = (1 << 31) + 64 * a  # elements: image 1 starts 4 GiB + 1 MB past image 0
+    storage = torch.empty(batch_stride + 64 * a, dtype=torch.float16, device=gpu)
+    far = storage.as_strided((2, 64, a), (batch_stride, a, 1))
+    near = (normal16((2, 64, a), 61) * 3).to(gpu)
+    far.copy_(near)
+    scores = normal16((2, 80, a), 62).to(gpu)
+    try:
+        for out_dtype in (torch.float16, torch.float32):
+            assert bits_equal(capi.dfl_expect(far, out_dtype).cpu(), capi.dfl_expect(near, out_dtype).cpu())
+        assert bits_equal(capi.detect_decode(far, scores, shapes, strides).cpu(),
+                          capi.detect_decode(near, scores, shapes, strides).cpu())
+    finally:
+        del far, storage
+        torch.cuda.empty_cache()

@@ -132,11 +132,11 @@ __device__ __forceinline__ float sigmoid_fast(float x) { return fast_rcp(1.0f + 
 
 // DFL expectation of V adjacent anchors: sum_i i * softmax_i(bins[i][j]) over
 // the 16 bins of one box side.  The bin max only stabilises the exponentials
-// (plain max: a NaN bin, a +inf bin or an all -inf side already makes the sum
-// NaN, as the CPU softmax then expectation does).  FAST (fp16 results):
-// e = exp2(x*log2e - m*log2e) as one fma (an error in the common term scales
-// every e_i alike and cancels in w/s) and w * 1/s; otherwise expf and an IEEE
-// division.
+// (NaN-propagating packed maximum: a NaN bin, a +inf bin or an all -inf side
+// makes the sum NaN either way, as the CPU softmax then expectation does).
+// FAST (fp16 results): e = exp2(x*log2e - m*log2e) as one fma (an error in the
+// common term scales every e_i alike and cancels in w/s) and w * 1/s;
+// otherwise expf and an IEEE division.  w accumulates with fma.
 template <int V, bool FAST>
 __device__ __forceinline__ void dfl_side(const _Float16 (&bins)[16][V], float (&r)[V]) {
   typedef _Float16 hv __attribute__((ext_vector_type(2)));
@@ -144,7 +144,7 @@ __device__ __forceinline__ void dfl_side(const _Float16 (&bins)[16][V], float (&
   if constexpr (V == 2) {
     hv mv = {bins[0][0], bins[0][1]};
 #pragma unroll
-    for (int i = 1; i < 16; ++i) mv = __builtin_elementwise_max(mv, (hv){bins[i][0], bins[i][1]});
+    for (int i = 1; i < 16; ++i) mv = __builtin_elementwise_maximum(mv, (hv){bins[i][0], bins[i][1]});
     m[0] = (float)mv[0];
     m[1] = (float)mv[1];
   } else {
@@ -165,7 +165,7 @@ __device__ __forceinline__ void dfl_side(const _Float16 (&bins)[16][V], float (&
       const float x = (float)bins[i][j];
       const float e = FAST ? __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -ml)) : expf(x - m[j]);
       s += e;
-      w += e * (float)i;
+      if (i > 0) w = __builtin_fmaf(e, (float)i, w);
     }
     if (FAST) {
       // Materialise the fp32 quotient: otherwise the backend may fold the
@@ -181,18 +181,46 @@ __device__ __forceinline__ void dfl_side(const _Float16 (&bins)[16][V], float (&
   }
 }
 
-// Loads the 16 bins (row stride xc) of V adjacent anchors starting at xp.
+// Loads the 16 bins of V adjacent anchors: bin i sits at byte offset
+// off + i * stride from base.
 template <int V>
-__device__ __forceinline__ void dfl_load(const _Float16* xp, int64_t xc, _Float16 (&bins)[16][V]) {
+__device__ __forceinline__ void dfl_load(const char* base, uint64_t off, uint64_t stride, _Float16 (&bins)[16][V]) {
   typedef _Float16 hv __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
+    const char* ptr = base + (off + i * stride);
     if constexpr (V == 2) {
-      const hv b = *reinterpret_cast<const hv*>(xp + i * xc);
+      const hv b = *reinterpret_cast<const hv*>(ptr);
       bins[i][0] = b[0];
       bins[i][1] = b[1];
     } else {
-      bins[i][0] = xp[i * xc];
+      bins[i][0] = *reinterpret_cast<const _Float16*>(ptr);
+    }
+  }
+}
+
+// Raw buffer resource over `bytes` bytes from base (gfx9 descriptor word 3);
+// loads at offsets >= bytes return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// The same 16 bins through a buffer resource: the per-bin offset i * stride is
+// uniform, so it travels as the scalar offset and a load needs no vector
+// address arithmetic.  NT: non-temporal (streaming) loads.
+template <int V, bool NT>
+__device__ __forceinline__ void dfl_load_buffer(__amdgpu_buffer_rsrc_t rsrc, uint32_t off, uint32_t stride,
+                                                _Float16 (&bins)[16][V]) {
+  typedef _Float16 hv __attribute__((ext_vector_type(2)));
+  constexpr int kAux = NT ? 2 : 0;  // cache-policy operand: 2 = nt
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (V == 2) {
+      const hv b = __builtin_bit_cast(hv, __builtin_amdgcn_raw_buffer_load_b32(rsrc, off, i * stride, kAux));
+      bins[i][0] = b[0];
+      bins[i][1] = b[1];
+    } else {
+      bins[i][0] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, i * stride, kAux));
     }
   }
 }

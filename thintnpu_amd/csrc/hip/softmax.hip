@@ -252,12 +252,16 @@ struct DflPlan {
   uint32_t avecs;       // A / V
   uint32_t units;       // sides * avecs
   FastDiv div_avecs;
+  uint32_t x_bytes;     // byte extent of x from its base (32-bit offset form)
 };
 
 // Thread per V (1 or 2) adjacent anchors of one box side; the math is
 // dev::dfl_side (shared with the detect-decode kernel, so both give the same
 // bits).
-template <typename TO, int V, bool FAST>
+// LOAD 0: 64-bit pointers.  LOAD 1/2: every byte offset into x fits 32 bits
+// (non-negative strides), so the bins are read through a buffer resource over
+// x_bytes; 2 adds streaming loads (launches of at least kStreamingBytes).
+template <typename TO, int V, bool FAST, int LOAD>
 __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
   static_assert(V == 1 || V == 2, "one or two anchors per thread");
   const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
@@ -265,9 +269,14 @@ __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
   const uint32_t side = p.div_avecs.div(u);
   const uint32_t a0 = (u - side * p.avecs) * V;
   const uint32_t n = side >> 2, sd = side & 3u;
-  const _Float16* xp = p.x + n * p.xn + (int64_t)(sd * 16) * p.xc + (int64_t)a0 * p.xa;
   _Float16 bins[16][V];
-  dev::dfl_load<V>(xp, p.xc, bins);
+  if constexpr (LOAD > 0) {
+    const uint32_t off = 2u * (n * (uint32_t)p.xn + sd * 16u * (uint32_t)p.xc + a0 * (uint32_t)p.xa);
+    dev::dfl_load_buffer<V, LOAD == 2>(dev::buffer_rsrc(p.x, p.x_bytes), off, 2u * (uint32_t)p.xc, bins);
+  } else {
+    const uint64_t off = 2 * (uint64_t)(n * p.xn + (int64_t)(sd * 16) * p.xc + (int64_t)a0 * p.xa);
+    dev::dfl_load<V>(reinterpret_cast<const char*>(p.x), off, 2 * (uint64_t)p.xc, bins);
+  }
   float r[V];
   dev::dfl_side<V, FAST>(bins, r);
   TO* op = static_cast<TO*>(p.out) + n * p.on + (int64_t)sd * p.os + (int64_t)a0 * p.oa;
@@ -310,11 +319,15 @@ struct DecodePlan {
   uint32_t score_units;   // B * nc * svecs
   FastDiv div_apairs, div_svecs, div_nc;
   int32_t xywh;
+  uint32_t boxes_bytes;   // byte extent of boxes from its base (buffer-load forms)
 };
 
 __device__ __forceinline__ _Float16 h_from_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
-template <int VB, int VS>
+// LOAD 0: 64-bit pointers.  LOAD 1/2: box offsets fit 32 bits and the bins
+// are read through a buffer resource; 2 also streams the score loads and the
+// output stores (launches of at least kStreamingBytes).
+template <int VB, int VS, int LOAD>
 __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
   if (blockIdx.x < p.box_blocks) {
     const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
@@ -322,13 +335,23 @@ __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
     const uint32_t ba_ = p.div_apairs.div(u);          // b * 2 + axis
     const uint32_t a0 = (u - ba_ * p.apairs) * VB;
     const uint32_t b = ba_ >> 1, axis = ba_ & 1u;
-    const _Float16* xb = p.boxes + b * p.bb + (int64_t)a0 * p.ba;
     _Float16 bins[16][VB];
     float lo[VB], hi[VB];
-    dev::dfl_load<VB>(xb + (int64_t)(axis * 16) * p.bc, p.bc, bins);
-    dev::dfl_side<VB, true>(bins, lo);
-    dev::dfl_load<VB>(xb + (int64_t)((axis + 2) * 16) * p.bc, p.bc, bins);
-    dev::dfl_side<VB, true>(bins, hi);
+    if constexpr (LOAD > 0) {
+      const __amdgpu_buffer_rsrc_t rs = dev::buffer_rsrc(p.boxes, p.boxes_bytes);
+      const uint32_t bc = 2u * (uint32_t)p.bc;
+      const uint32_t off = 2u * (b * (uint32_t)p.bb + a0 * (uint32_t)p.ba) + axis * 16u * bc;
+      dev::dfl_load_buffer<VB, LOAD == 2>(rs, off, bc, bins);
+      dev::dfl_side<VB, true>(bins, lo);
+      dev::dfl_load_buffer<VB, LOAD == 2>(rs, off + 32u * bc, bc, bins);
+      dev::dfl_side<VB, true>(bins, hi);
+    } else {
+      const char* xc = reinterpret_cast<const char*>(p.boxes + b * p.bb + (int64_t)a0 * p.ba);
+      dev::dfl_load<VB>(xc, 2 * (uint64_t)((int64_t)(axis * 16) * p.bc), 2 * (uint64_t)p.bc, bins);
+      dev::dfl_side<VB, true>(bins, lo);
+      dev::dfl_load<VB>(xc, 2 * (uint64_t)((int64_t)((axis + 2) * 16) * p.bc), 2 * (uint64_t)p.bc, bins);
+      dev::dfl_side<VB, true>(bins, hi);
+    }
     _Float16 first[VB], second[VB];
 #pragma unroll
     for (int j = 0; j < VB; ++j) {
@@ -352,8 +375,15 @@ __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
     _Float16* o = p.out + b * p.ob + (int64_t)a0 * p.oa;
     if constexpr (VB == 2) {
       typedef _Float16 hv __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<hv*>(o + (int64_t)axis * p.oc) = (hv){first[0], first[1]};
-      *reinterpret_cast<hv*>(o + (int64_t)(axis + 2) * p.oc) = (hv){second[0], second[1]};
+      hv* o1 = reinterpret_cast<hv*>(o + (int64_t)axis * p.oc);
+      hv* o2 = reinterpret_cast<hv*>(o + (int64_t)(axis + 2) * p.oc);
+      if constexpr (LOAD == 2) {
+        __builtin_nontemporal_store((hv){first[0], first[1]}, o1);
+        __builtin_nontemporal_store((hv){second[0], second[1]}, o2);
+      } else {
+        *o1 = (hv){first[0], first[1]};
+        *o2 = (hv){second[0], second[1]};
+      }
     } else {
       o[(int64_t)axis * p.oc] = first[0];
       o[(int64_t)(axis + 2) * p.oc] = second[0];
@@ -368,11 +398,13 @@ __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
   const _Float16* sp = p.scores + b * p.sb + (int64_t)c * p.sc + (int64_t)a0 * p.sa;
   _Float16* op = p.out + b * p.ob + (int64_t)(4 + c) * p.oc + (int64_t)a0 * p.oa;
   if constexpr (VS == 8) {
-    const dev::h8 x = *reinterpret_cast<const dev::h8*>(sp);
+    const dev::h8* src = reinterpret_cast<const dev::h8*>(sp);
+    const dev::h8 x = LOAD == 2 ? __builtin_nontemporal_load(src) : *src;
     dev::h8 y;
 #pragma unroll
     for (int j = 0; j < 8; ++j) y[j] = (_Float16)dev::sigmoid_fast((float)x[j]);
-    *reinterpret_cast<dev::h8*>(op) = y;
+    if constexpr (LOAD == 2) __builtin_nontemporal_store(y, reinterpret_cast<dev::h8*>(op));
+    else *reinterpret_cast<dev::h8*>(op) = y;
   } else {
     op[0] = (_Float16)dev::sigmoid_fast((float)sp[0]);
   }
@@ -543,13 +575,30 @@ extern "C" thin_status thin_dfl_expect(const thin_desc* x, const thin_desc* out,
   p.units = (uint32_t)units;
   p.div_avecs = FastDiv::make(p.avecs);
   const uint32_t grid = (p.units + kThreads - 1) / kThreads;
-  if (out->dtype == THIN_F16) {
-    if (vec) hipLaunchKernelGGL((dfl_expect_kernel<_Float16, V, true>), dim3(grid), dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL((dfl_expect_kernel<_Float16, 1, true>), dim3(grid), dim3(kThreads), 0, stream, p);
-  } else {
-    if (vec) hipLaunchKernelGGL((dfl_expect_kernel<float, V, false>), dim3(grid), dim3(kThreads), 0, stream, p);
-    else hipLaunchKernelGGL((dfl_expect_kernel<float, 1, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+  // 32-bit byte offsets when the whole of x lies within 4 GiB of its base
+  bool o32 = true;
+  uint64_t extent = 2;
+  for (int i = 0; i < 3; ++i) {
+    if (x->strides[i] < 0) o32 = false;
+    else extent += 2 * (uint64_t)(x->sizes[i] - 1) * (uint64_t)x->strides[i];
   }
+  o32 = o32 && extent < (1ull << 32);
+  p.x_bytes = o32 ? (uint32_t)extent : 0u;
+  const bool nt = (int64_t)p.sides * 16 * A * 2 >= kStreamingBytes;
+#define THIN_DFL(TO, VV, FAST)                                                                                    \
+  do {                                                                                                            \
+    if (o32 && nt) hipLaunchKernelGGL((dfl_expect_kernel<TO, VV, FAST, 2>), dim3(grid), dim3(kThreads), 0, stream, p); \
+    else if (o32) hipLaunchKernelGGL((dfl_expect_kernel<TO, VV, FAST, 1>), dim3(grid), dim3(kThreads), 0, stream, p);  \
+    else hipLaunchKernelGGL((dfl_expect_kernel<TO, VV, FAST, 0>), dim3(grid), dim3(kThreads), 0, stream, p);           \
+  } while (0)
+  if (out->dtype == THIN_F16) {
+    if (vec) THIN_DFL(_Float16, V, true);
+    else THIN_DFL(_Float16, 1, true);
+  } else {
+    if (vec) THIN_DFL(float, V, false);
+    else THIN_DFL(float, 1, false);
+  }
+#undef THIN_DFL
   THIN_LAUNCH_CHECK("dfl_expect");
   return THIN_OK;
 }
@@ -612,10 +661,27 @@ extern "C" thin_status thin_detect_decode(const thin_desc* boxes, const thin_des
   p.div_svecs = FastDiv::make(p.svecs);
   p.div_nc = FastDiv::make((uint32_t)nc);
   const uint32_t grid = p.box_blocks + (uint32_t)((score_units + kThreads - 1) / kThreads);
-  if (vb && vs) hipLaunchKernelGGL((detect_decode_kernel<2, 8>), dim3(grid), dim3(kThreads), 0, stream, p);
-  else if (vb) hipLaunchKernelGGL((detect_decode_kernel<2, 1>), dim3(grid), dim3(kThreads), 0, stream, p);
-  else if (vs) hipLaunchKernelGGL((detect_decode_kernel<1, 8>), dim3(grid), dim3(kThreads), 0, stream, p);
-  else hipLaunchKernelGGL((detect_decode_kernel<1, 1>), dim3(grid), dim3(kThreads), 0, stream, p);
+  // 32-bit box offsets (buffer loads) when boxes lie within 4 GiB of their base
+  bool o32 = true;
+  uint64_t extent = 2;
+  for (int i = 0; i < 3; ++i) {
+    if (boxes->strides[i] < 0) o32 = false;
+    else extent += 2 * (uint64_t)(boxes->sizes[i] - 1) * (uint64_t)boxes->strides[i];
+  }
+  o32 = o32 && extent < (1ull << 32);
+  p.boxes_bytes = o32 ? (uint32_t)extent : 0u;
+  const int load = !o32 ? 0 : numel(out) * 2 >= kStreamingBytes ? 2 : 1;
+#define THIN_DECODE(B_, S_)                                                                                      \
+  do {                                                                                                           \
+    if (load == 2) hipLaunchKernelGGL((detect_decode_kernel<B_, S_, 2>), dim3(grid), dim3(kThreads), 0, stream, p); \
+    else if (load == 1) hipLaunchKernelGGL((detect_decode_kernel<B_, S_, 1>), dim3(grid), dim3(kThreads), 0, stream, p); \
+    else hipLaunchKernelGGL((detect_decode_kernel<B_, S_, 0>), dim3(grid), dim3(kThreads), 0, stream, p);           \
+  } while (0)
+  if (vb && vs) THIN_DECODE(2, 8);
+  else if (vb) THIN_DECODE(2, 1);
+  else if (vs) THIN_DECODE(1, 8);
+  else THIN_DECODE(1, 1);
+#undef THIN_DECODE
   THIN_LAUNCH_CHECK("detect_decode");
   return THIN_OK;
 }
