@@ -56,6 +56,14 @@ def fixtures(full=True):
         yield f"class-block-{nc}", predictions(2, 144, nc, seed=1000 + nc), 129, False, "transposed", False
     for agnostic in (False, True):  # more anchors than one block holds in registers
         yield f"large-anchors-{agnostic}", predictions(1, 40000, 2, seed=41), 300, agnostic, "transposed", False
+    # pair selection where most of the K x nc pairs tie the first stage's
+    # threshold: every pair (all scores equal), or thousands (five score levels)
+    g = _g(77)
+    tied = torch.cat((torch.randn(1, 400, 4, generator=g).half(), torch.ones(1, 400, 80).half()), -1)
+    yield "tied-pairs", tied, 300, False, "transposed", False
+    coarse = torch.randint(0, 5, (1, 1000, 80), generator=g).half() / 4
+    yield "coarse-scores", torch.cat((torch.randn(1, 1000, 4, generator=g).half(), coarse), -1), 300, False, \
+        "transposed", False
     if full:
         patterns = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16)
         x = torch.cat((torch.zeros(1, 128, 4).half(), patterns.reshape(1, 128, 512)), -1)

@@ -210,15 +210,22 @@ __global__ __launch_bounds__(kSelThreads) void topk_block_kernel(TopkPlan p) {
 // One 1024-thread block per batch for up to 32768 candidates.  The candidate
 // bits are staged in LDS with coalesced 16-byte loads (they also serve the
 // packing step), then thread t takes candidates [t*KPT, t*KPT + KPT) into
-// registers, so thread order is index order.  Radix select: per-wave LDS histograms of the high and
-// then the low key byte, summed and scanned by 256 threads, give the threshold
-// key T and how many T-keyed candidates to keep; a block-wide exclusive scan of
-// per-thread T counts ranks the T-keyed candidates in index order (lowest index
-// kept).  The K selected records (key << 16 | index, unique) are ordered by
-// rank counting (K <= 512) or an LDS bitonic sort.  Modes: 0 writes the
-// selected indices; 1 (class-agnostic anchors) and 2 (per-class pairs, whose
-// scores a wide gather kernel collected) also pack the output rows and the
-// trace stages.
+// registers, so thread order is index order.  Radix select: per-wave LDS
+// histograms of the high and then the low key byte, summed and scanned by 256
+// threads, give the threshold key T and how many T-keyed candidates to keep; a
+// block-wide exclusive scan of per-thread T counts ranks the T-keyed
+// candidates in index order (lowest index kept).  The K selected records
+// (key << 16 | index, unique) are ordered by rank counting (K <= 512, each
+// record's rank summed over several threads) or an LDS bitonic sort.
+// Modes: 0 writes the selected indices and the threshold key T; 1
+// (class-agnostic anchors) and 2 (per-class pairs, whose scores a wide gather
+// kernel collected) also pack the output rows and the trace stages.
+//
+// Mode 2 survivors: the K anchors of the first stage carry K pairs (their
+// class maxima) keyed at most T1, the first stage's threshold, so the K-th
+// best pair is keyed at most T1 and pairs keyed above it are never selected;
+// they are dropped before the histograms.  Mode 2 with K <= 512 also fetches
+// the first-stage anchors and their boxes into LDS while the selection runs.
 constexpr uint32_t kRegThreads = 1024;
 constexpr uint32_t kRegWaves = kRegThreads / 64;
 constexpr uint32_t kRegMaxN = 32768;
@@ -233,10 +240,31 @@ struct RegTopkPlan {
   FastDiv nc;             // classes (mode 2 pair index = rank * nc + class)
   int64_t anchors;        // row pitch of bits1 / cls1 (mode 1)
   int32_t* sel;           // mode 0: [B, K] selected candidate indices
+  uint32_t* thresh;       // mode 0 writes, mode 2 reads (if set): threshold key per batch
   const int32_t* cls1;    // mode 1: class-max labels [B, A]
   uint32_t* out;          // modes 1, 2: [B, K, 6] fp32 bits
   thin_select_trace tr;
 };
+
+// LDS slot of candidate i.  Thread t reads its KPT keys as KPT/8 16-byte
+// vectors at a stride of KPT*2 bytes; the vectors of one thread are permuted
+// by a function of t so that the lanes of one read instruction fall on
+// distinct bank groups for 128- and 256-byte LDS rows alike.
+template <int KPT>
+__device__ __forceinline__ uint32_t staged_vec(uint32_t g) {
+  constexpr uint32_t VPT = KPT / 8;
+  if constexpr (VPT == 1) {
+    return g;
+  } else {
+    const uint32_t t = g / VPT, v = g % VPT;
+    const uint32_t f = VPT == 4 ? ((t >> 1) ^ (t >> 3)) & 3u : ((t >> 2) ^ (t >> 3)) & 1u;
+    return t * VPT + (v ^ f);
+  }
+}
+template <int KPT>
+__device__ __forceinline__ uint32_t staged_slot(uint32_t i) {
+  return (staged_vec<KPT>(i >> 3) << 3) | (i & 7u);
+}
 
 // Exclusive block-wide prefix sum of v; `total` receives the block sum.
 __device__ __forceinline__ uint32_t block_exclusive_sum(uint32_t v, uint32_t* wave_tot, uint32_t& total) {
@@ -280,26 +308,41 @@ __device__ __forceinline__ void pick_bin(uint32_t (*hist)[256], uint32_t base, u
   __syncthreads();
 }
 
+// First-stage anchors and their box bits, fetched into LDS by mode 2.
+struct PairBoxes {
+  int32_t anchor[kRankSortMax];
+  uint16_t box[kRankSortMax][4];
+};
+
 // Output row r of batch b for selected candidate idx; `staged` holds the
-// batch's candidate bits (the selected score's bits are staged[idx]).
-template <int MODE>
-__device__ __forceinline__ void pack_row(const RegTopkPlan& p, const uint16_t* staged, uint32_t b, uint32_t r,
-                                         uint32_t idx) {
+// batch's candidate bits (the selected score's bits are at staged_slot(idx)).
+template <int MODE, int KPT>
+__device__ __forceinline__ void pack_row(const RegTopkPlan& p, const uint16_t* staged, const PairBoxes* pb,
+                                         uint32_t b, uint32_t r, uint32_t idx) {
   int64_t a, label;
-  const uint32_t sbits = staged[idx];
+  const uint32_t sbits = staged[staged_slot<KPT>(idx)];
+  uint32_t box[4];
   if (MODE == 1) {
     a = idx;
     label = p.cls1[(int64_t)b * p.anchors + a];
   } else {
     const uint32_t rank1 = p.nc.div(idx);
     label = idx - rank1 * p.nc.d;
-    a = p.stage1[(size_t)b * p.K + rank1];
+    a = pb ? pb->anchor[rank1] : p.stage1[(size_t)b * p.K + rank1];
+    if (pb) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) box[c] = pb->box[rank1][c];
+    }
   }
-  const uint16_t* box = p.L.x + b * p.L.sb + a * p.L.sa;
+  if (MODE == 1 || !pb) {
+    const uint16_t* bx = p.L.x + b * p.L.sb + a * p.L.sa;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) box[c] = bx[c * p.L.sc];
+  }
   const size_t t = (size_t)b * p.K + r;
   uint32_t* o = p.out + t * 6;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) o[c] = float_bits(box[c * p.L.sc]);
+  for (int c = 0; c < 4; ++c) o[c] = float_bits(box[c]);
   o[4] = float_bits(sbits);
   o[5] = __float_as_uint((float)label);
   if (p.tr.stage1) static_cast<int64_t*>(p.tr.stage1)[t] = MODE == 1 ? a : (int64_t)p.stage1[t];
@@ -331,67 +374,65 @@ __device__ __forceinline__ void count_bins(uint32_t* hist, const uint32_t (&key)
   if (run) atomicAdd(&hist[cur], run);
 }
 
-template <int MODE, int KPT>
-__global__ __launch_bounds__(kRegThreads) void topk_reg_kernel(RegTopkPlan p) {
+// ranks[r] (zero on entry) += the number of records below rec[r], for
+// r < count; rec[count, n16) are 0xffffffff pads and n16 <= 512 is a multiple
+// of 16.  Records are unique, so the ranks are a permutation.  A record's rank
+// is summed over kRegThreads / n16 threads, each comparing a slice of the
+// records, 16 per step.  Ends with a block barrier.
+__device__ __forceinline__ void rank_records(const uint32_t* rec, uint32_t n16, uint32_t count, uint32_t* ranks) {
   typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-  __shared__ __attribute__((aligned(16))) uint16_t staged[kRegMaxN];
-  __shared__ uint32_t hist[kRegWaves][256];
-  __shared__ __attribute__((aligned(16))) uint32_t recs[kRegMaxK];
-  __shared__ uint32_t wave_tot[kRegWaves];
-  __shared__ uint32_t result[2];
-  const uint32_t b = blockIdx.x, tid = threadIdx.x, wave = tid >> 6;
-  const uint32_t n = p.n, K = p.K;
-  const uint32_t first = tid * KPT;
-
-  // stage the batch's candidate bits in LDS (coalesced), then take this
-  // thread's KPT consecutive keys (0xffffffff past the end)
-  const uint16_t* src = p.bits + (size_t)b * n;
-  uint32_t head = 0;
-  if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
-    head = n & ~7u;
-    for (uint32_t v = tid; v < head / 8; v += kRegThreads)
-      reinterpret_cast<u4*>(staged)[v] = reinterpret_cast<const u4*>(src)[v];
-  }
-  for (uint32_t i = head + tid; i < n; i += kRegThreads) staged[i] = src[i];
-  __syncthreads();
-  uint32_t key[KPT];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t parts = kRegThreads / n16;  // >= 2 since n16 <= 512
+  const uint32_t slice = ((n16 / 4 + parts - 1) / parts + 3) & ~3u;  // u4 records per thread
+  const uint32_t r = tid % n16, part = tid / n16;
+  if (part < parts) {
+    const uint32_t mine = rec[r];
+    const u4* r4 = reinterpret_cast<const u4*>(rec);
+    const uint32_t lo = part * slice, hi = min(lo + slice, n16 / 4);
+    uint32_t rank = 0;
+    for (uint32_t u = lo; u < hi; u += 4) {
+      u4 q[4];
 #pragma unroll
-  for (int v = 0; v < KPT / 8; ++v) {
-    const u4 w = reinterpret_cast<const u4*>(staged + first)[v];
+      for (int h = 0; h < 4; ++h) q[h] = r4[u + h];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      key[v * 8 + 2 * h] = w[h] & 0xffffu;
-      key[v * 8 + 2 * h + 1] = w[h] >> 16;
+      for (int h = 0; h < 4; ++h)
+        rank += (q[h].x < mine) + (q[h].y < mine) + (q[h].z < mine) + (q[h].w < mine);
     }
+    if (r < count && rank) atomicAdd(&ranks[r], rank);
   }
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) key[j] = first + j < n ? score_key(key[j]) : 0xffffffffu;
+  __syncthreads();
+}
 
+// Radix-selects the K best candidates: thread t holds N keys (0xffffffff =
+// absent) of candidates idx[j], and the block-wide order (t, j) is index
+// order.  hist[0] and hist[1] must be zero.  Writes the K records
+// (key << 16 | index) to recs[0, K) and returns the threshold key T.
+template <int N>
+__device__ __forceinline__ uint32_t radix_select(uint32_t (&key)[N], const uint32_t (&idx)[N], uint32_t K,
+                                                 uint32_t (*hist)[kRegWaves][256], uint32_t* wave_tot,
+                                                 uint32_t* result, uint32_t* recs) {
+  const uint32_t wave = threadIdx.x >> 6;
   // level 1: high byte
-  for (uint32_t q = tid; q < kRegWaves * 256; q += kRegThreads) (&hist[0][0])[q] = 0;
+  count_bins<N>(hist[0][wave], key, 0xffffffffu);
   __syncthreads();
-  count_bins<KPT>(hist[wave], key, 0xffffffffu);
-  __syncthreads();
-  pick_bin(hist, 0, K, wave_tot, result);
+  pick_bin(hist[0], 0, K, wave_tot, result);
   const uint32_t b1 = result[0], below1 = result[1];
   // level 2: low byte inside bucket b1
-  for (uint32_t q = tid; q < kRegWaves * 256; q += kRegThreads) (&hist[0][0])[q] = 0;
+  count_bins<N>(hist[1][wave], key, b1);
   __syncthreads();
-  count_bins<KPT>(hist[wave], key, b1);
-  __syncthreads();
-  pick_bin(hist, below1, K, wave_tot, result);
+  pick_bin(hist[1], below1, K, wave_tot, result);
   const uint32_t T = (b1 << 8) | result[0];
   const uint32_t need = K - result[1];  // T-keyed candidates kept, lowest index first
 
   // rank the T-keyed candidates in index order, then place the selected ones
   uint32_t eq = 0;
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) eq += key[j] == T ? 1u : 0u;
+  for (int j = 0; j < N; ++j) eq += key[j] == T ? 1u : 0u;
   uint32_t total;
   uint32_t eq_before = block_exclusive_sum(eq, wave_tot, total);
   uint32_t mine = 0;
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
+  for (int j = 0; j < N; ++j) {
     const bool take = key[j] < T || (key[j] == T && eq_before < need);
     eq_before += key[j] == T ? 1u : 0u;
     key[j] = take ? key[j] : 0xffffffffu;  // reuse: 0xffffffff = not selected
@@ -399,32 +440,119 @@ __global__ __launch_bounds__(kRegThreads) void topk_reg_kernel(RegTopkPlan p) {
   }
   uint32_t pos = block_exclusive_sum(mine, wave_tot, total);
 #pragma unroll
-  for (int j = 0; j < KPT; ++j)
-    if (key[j] != 0xffffffffu) recs[pos++] = (key[j] << 16) | (first + j);
+  for (int j = 0; j < N; ++j)
+    if (key[j] != 0xffffffffu) recs[pos++] = (key[j] << 16) | idx[j];
+  return T;
+}
+
+template <int MODE, int KPT>
+__global__ __launch_bounds__(kRegThreads) void topk_reg_kernel(RegTopkPlan p) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) uint16_t staged[kRegMaxN];
+  __shared__ uint32_t hist[2][kRegWaves][256];
+  __shared__ __attribute__((aligned(16))) uint32_t recs[kRegMaxK];
+  __shared__ uint32_t ranks[kRankSortMax];
+  __shared__ __attribute__((aligned(16))) uint32_t surv[MODE == 2 ? kRegThreads : 16];
+  __shared__ PairBoxes pbox;
+  __shared__ uint32_t wave_tot[kRegWaves];
+  __shared__ uint32_t result[2];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x;
+  const uint32_t n = p.n, K = p.K;
+  const uint32_t first = tid * KPT;
+  const bool prefetch = MODE == 2 && K <= kRankSortMax;
+
+  // mode 2: the first-stage anchors, then (below) their boxes, into LDS
+  if (prefetch && tid < K) pbox.anchor[tid] = p.stage1[(size_t)b * K + tid];
+  // stage the batch's candidate bits in LDS (coalesced), clear both
+  // histograms and the partial ranks
+  const uint16_t* src = p.bits + (size_t)b * n;
+  uint32_t head = 0;
+  if ((reinterpret_cast<uintptr_t>(src) & 15u) == 0) {
+    head = n & ~7u;
+    for (uint32_t v = tid; v < head / 8; v += kRegThreads)
+      reinterpret_cast<u4*>(staged)[staged_vec<KPT>(v)] = reinterpret_cast<const u4*>(src)[v];
+  }
+  for (uint32_t i = head + tid; i < n; i += kRegThreads) staged[staged_slot<KPT>(i)] = src[i];
+  for (uint32_t q = tid; q < 2 * kRegWaves * 256; q += kRegThreads) (&hist[0][0][0])[q] = 0;
+  for (uint32_t q = tid; q < kRankSortMax; q += kRegThreads) ranks[q] = 0;
+  const uint32_t t1 = MODE == 2 && p.thresh ? p.thresh[b] : 0xffffu;
+  __syncthreads();
+  // box bits of the first-stage anchors: the loads stay in flight during the
+  // selection and land in LDS just before the packing
+  uint32_t box_bits[4] = {0u, 0u, 0u, 0u};
+  if (prefetch && tid < K) {
+    const uint16_t* bx = p.L.x + b * p.L.sb + (int64_t)pbox.anchor[tid] * p.L.sa;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) box_bits[c] = bx[c * p.L.sc];
+  }
+  uint32_t key[KPT], idx[KPT];
+#pragma unroll
+  for (int v = 0; v < KPT / 8; ++v) {
+    const u4 w = reinterpret_cast<const u4*>(staged)[staged_vec<KPT>(tid * (KPT / 8) + v)];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      key[v * 8 + 2 * h] = w[h] & 0xffffu;
+      key[v * 8 + 2 * h + 1] = w[h] >> 16;
+    }
+  }
+  uint32_t survivors = 0;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const uint32_t k = first + j < n ? score_key(key[j]) : 0xffffffffu;
+    key[j] = k <= t1 ? k : 0xffffffffu;  // mode 2: pairs keyed above T1 are never selected
+    idx[j] = first + j;
+    survivors += key[j] != 0xffffffffu ? 1u : 0u;
+  }
+
+  uint32_t T = 0;
+  bool compact = false;
+  if constexpr (MODE == 2) {
+    // few survivors: move their records (in index order) to LDS
+    uint32_t count;
+    uint32_t at = block_exclusive_sum(survivors, wave_tot, count);
+    compact = count <= kRegThreads;
+    if (compact) {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j)
+        if (key[j] != 0xffffffffu) surv[at++] = (key[j] << 16) | (first + j);
+      const uint32_t C16 = (count + 15u) & ~15u;
+      if (count <= kRankSortMax && tid >= count && tid < C16) surv[tid] = 0xffffffffu;
+      __syncthreads();
+      if (count <= kRankSortMax) {
+        // at most 512: a survivor's rank among all survivors (records are
+        // unique) is its output row; ranks below K are the selection, sorted
+        rank_records(surv, C16, count, ranks);
+        if (tid < count && ranks[tid] < K) recs[ranks[tid]] = surv[tid];
+        if (prefetch && tid < K) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) pbox.box[tid][c] = (uint16_t)box_bits[c];
+        }
+        __syncthreads();
+        if (tid < K) pack_row<MODE, KPT>(p, staged, &pbox, b, tid, recs[tid] & 0xffffu);
+        return;
+      }
+      uint32_t k1[1] = {tid < count ? surv[tid] >> 16 : 0xffffffffu};
+      const uint32_t i1[1] = {tid < count ? surv[tid] & 0xffffu : 0u};
+      T = radix_select<1>(k1, i1, K, hist, wave_tot, result, recs);
+    }
+  }
+  if (!compact) T = radix_select<KPT>(key, idx, K, hist, wave_tot, result, recs);
+  if (MODE == 0 && p.thresh && tid == 0) p.thresh[b] = T;
+  const uint32_t K16 = (K + 15u) & ~15u;
+  if (K <= kRankSortMax && tid >= K && tid < K16) recs[tid] = 0xffffffffu;
+  if (prefetch && tid < K) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) pbox.box[tid][c] = (uint16_t)box_bits[c];
+  }
   __syncthreads();
 
+  const PairBoxes* pb = prefetch ? &pbox : nullptr;
   if (K <= kRankSortMax) {
-    // rank counting: records are unique, so ranks are a permutation; the pad
-    // up to a multiple of 16 (0xffffffff) is above every record
-    const uint32_t K16 = (K + 15u) & ~15u;
-    if (tid >= K && tid < K16) recs[tid] = 0xffffffffu;
-    __syncthreads();
+    rank_records(recs, K16, K, ranks);
     if (tid < K) {
-      const uint32_t rec = recs[tid];
-      uint32_t rank = 0;
-      typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-      const u4* r4 = reinterpret_cast<const u4*>(recs);
-      for (uint32_t u = 0; u < K16 / 4; u += 4) {
-        u4 q[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) q[h] = r4[u + h];
-#pragma unroll
-        for (int h = 0; h < 4; ++h)
-          rank += (q[h].x < rec) + (q[h].y < rec) + (q[h].z < rec) + (q[h].w < rec);
-      }
-      const uint32_t idx = rec & 0xffffu;
-      if (MODE == 0) p.sel[(size_t)b * K + rank] = (int32_t)idx;
-      else pack_row<MODE>(p, staged, b, rank, idx);
+      const uint32_t idx = recs[tid] & 0xffffu;
+      if (MODE == 0) p.sel[(size_t)b * K + ranks[tid]] = (int32_t)idx;
+      else pack_row<MODE, KPT>(p, staged, pb, b, ranks[tid], idx);
     }
     return;
   }
@@ -451,7 +579,7 @@ __global__ __launch_bounds__(kRegThreads) void topk_reg_kernel(RegTopkPlan p) {
   for (uint32_t r = tid; r < K; r += kRegThreads) {
     const uint32_t idx = recs[r] & 0xffffu;
     if (MODE == 0) p.sel[(size_t)b * K + r] = (int32_t)idx;
-    else pack_row<MODE>(p, staged, b, r, idx);
+    else pack_row<MODE, KPT>(p, staged, pb, b, r, idx);
   }
 }
 
@@ -567,7 +695,7 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackArgs p) {
 // ---------------------------------------------------------------- host
 
 struct WsLayout {
-  size_t bits1, cls1, stage1, gathered, stage2, recs, total;
+  size_t bits1, cls1, stage1, gathered, stage2, thresh, recs, total;
   uint32_t recs_pitch;  // P for the large-K path (0 = not needed)
 };
 
@@ -584,6 +712,7 @@ WsLayout ws_layout(int64_t B, int64_t A, int64_t nc, int64_t max_det, bool agnos
   if (!agnostic) {
     w.gathered = off; off += up256((size_t)(B * K * nc) * 2);
     w.stage2 = off; off += up256((size_t)(B * K) * 4);
+    w.thresh = off; off += up256((size_t)B * 4);
   }
   if (K > (int64_t)kLdsSort) {
     const int64_t n = agnostic ? A : (A > K * nc ? A : K * nc);
@@ -699,6 +828,7 @@ extern "C" thin_status thin_detection_select(const thin_desc* decoded, int64_t m
     rp.bits = bits1;
     rp.n = (uint32_t)A;
     rp.sel = stage1;
+    rp.thresh = agn ? nullptr : reinterpret_cast<uint32_t*>(ws + w.thresh);  // T1 for the pair survivors
     launch_reg_topk<0>(rp, B, stream);
     THIN_LAUNCH_CHECK("topk_stage1");
   } else {
