@@ -135,9 +135,18 @@ def test_glue_registers_privateuse1():
                "thin_native_flow::pack_input", "thin_native_flow::maxpool", "thin_backend::maxpool2d",
                "aten::max_pool2d_with_indices", "aten::fill_.Scalar", "aten::zero_",
                "thin_native_flow::detection_select", "thin_native_flow::detection_select_trace",
-               "thin_blocked::pack", "thin_blocked::unpack"):
+               "thin_blocked::pack", "thin_blocked::unpack", "aten::split_with_sizes", "aten::arange.start_out",
+               "aten::arange.out", "aten::_local_scalar_dense", "aten::bmm", "thin_backend::nms",
+               "thin_backend::conv2d", "thin_native_flow::conv", "thin_native_flow::stem",
+               "thin_native_flow::bmm", "thin_native_flow::layout_bmm", "thin_native_flow::channel_select",
+               "thin_native_flow::depthwise", "thin_blocked::conv"):
         assert has(op, "PrivateUse1"), op
     assert hasattr(torch.classes.thin_backend, "RuntimeGraph")
+    # plan takes no tensors: a catch-all kernel, as conv_flow.cpp:631 defines it
+    assert has("thin_native_flow::plan", "CompositeImplicitAutograd")
+    for op in ("thin_backend::add", "thin_backend::sigmoid", "thin_backend::upsample_nearest2d",
+               "thin_backend::maxpool2d"):
+        assert has(op, "Meta"), op
 
 
 def test_fused_meta_shapes():

@@ -129,7 +129,8 @@ def test_aten_routes_and_rejects(npu):
         for name, op in (("conv", lambda: F.conv2d(an, torch.randn(3, 7, 3, 3).to(npu))),
                          ("pool-k3", lambda: F.max_pool2d(an, 3, 1, 1)),
                          ("pool-s2", lambda: F.max_pool2d(an, 5, 2, 2)),
-                         ("nearest-3x", lambda: F.interpolate(an, scale_factor=3, mode="nearest"))):
+                         ("nearest-3x", lambda: F.interpolate(an, scale_factor=3, mode="nearest")),
+                         ("bmm", lambda: torch.bmm(an[0], an[0]))):
             with pytest.raises(RuntimeError, match="thin aten"):
                 op()
 
