@@ -430,9 +430,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op table")
     ap.add_argument("--iters", type=int, default=200, help="launches per per-op timing round")
-    ap.add_argument("--profile", choices=["dominant", "copy"], default=None,
-                    help="only replay the dominant kernel, or a plain 16-byte copy of the same size "
-                         "(rocprofv3 summaries / counter calibration); prints its timing")
+    ap.add_argument("--profile", default=None,
+                    help="replay one kernel only and print its timing (rocprofv3 summaries / counter "
+                         "calibration): 'dominant', 'copy' (a plain 16-byte copy of the same size), or "
+                         "'op:<row name>[@N]' for one row of the per-op table (N=32 by default, rotated)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of "
@@ -445,7 +446,22 @@ def main():
     capi.lib()
     dev = torch.device("cuda:0")
     n = 32
+    if args.profile and args.profile.startswith("op:"):
+        name, _, nn = args.profile[3:].partition("@")
+        nn = int(nn) if nn else (1 if name.startswith("detection_select") else 32)
+        found = [f for (rname, _, rn, f) in op_rows(capi, dev) if rname == name and rn == nn]
+        if not found:
+            print(f"no op row {name!r} at N={nn}", file=sys.stderr)
+            sys.exit(2)
+        launch, sets, algo = found[0](not name.startswith("detection_select"))
+        t = time_launches(launch, sets, args.iters)
+        print(json.dumps({"profile": f"{name} N={nn}", "us": round(t * 1e6, 3), "GB/s": round(algo / t / 1e9, 1),
+                          "bytes": algo}))
+        return
     if args.profile:
+        if args.profile not in ("dominant", "copy"):
+            print(f"unknown --profile {args.profile!r}", file=sys.stderr)
+            sys.exit(2)
         launch, sets, algo = op_affine_silu(capi, dev, n, *C2_SHAPES[0], False, rotate=True)
         what = "affine_silu N=32 C,H,W=(128,80,80)"
         if args.profile == "copy":
