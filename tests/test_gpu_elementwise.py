@@ -280,3 +280,25 @@ def test_transpose_copy(gpu, dtype):
         got = torch.empty(src.shape, dtype=dtype, device=gpu)
         capi.copy(x.to(gpu).permute(*perm), got)
         assert torch.equal(got.cpu().view(torch.uint8), src.contiguous().view(torch.uint8))
+
+
+def test_beyond_32bit_extents(gpu):
+    """Operands past 2^31 elements (4 GiB of fp16) run as several launches over
+    slabs whose offsets fit 32 bits: a contiguous 1-D add across the slab
+    boundaries, and a column slice of a [33000, 65536] tensor whose span passes
+    2^31.  Small integers keep every result exact, so torch's own device ops are
+    an exact reference at this size."""
+    from thintnpu_amd import capi
+    n = (1 << 31) + 4096 + 8
+    x = (torch.arange(n, device=gpu, dtype=torch.int32) % 2039).to(torch.float16)
+    y = torch.full((1,), 3.0, dtype=torch.float16, device=gpu)
+    got = capi.binary(capi.ADD, x, y, alpha=2.0)
+    assert torch.equal(got, x + 6)
+    del got, x
+    torch.cuda.empty_cache()
+    rows, cols = 33000, 65536
+    base = (torch.arange(rows * cols, device=gpu, dtype=torch.int32) % 1021).to(torch.float16).view(rows, cols)
+    view = base[:, 16:]
+    assert torch.equal(capi.binary_scalar(capi.MUL, view, 2.0), view * 2)
+    del base, view
+    torch.cuda.empty_cache()

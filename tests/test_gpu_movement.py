@@ -309,3 +309,16 @@ def test_maxpool_wide_rows(gpu, c, h, w, k):
     check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"{c}x{h}x{w} k{k}")
     y = pool_specials(normal16((1, 3, h, w * 5), k))
     check_pool(capi.maxpool2d_nchw(y.to(gpu), k).cpu(), mv.maxpool_nchw(y, k), f"nchw {h}x{w * 5} k{k}")
+
+
+def test_cat_beyond_4gib(gpu):
+    """A cat whose output passes 4 GiB (the second input lands 2 GiB in): the
+    row and column offsets are 64-bit.  Small integers make torch.cat on the
+    device an exact reference at this size."""
+    from thintnpu_amd import capi
+    half = (1 << 30) + 64
+    a = (torch.arange(half, device=gpu, dtype=torch.int32) % 2039).to(torch.float16).view(1, half)
+    b = (torch.arange(half, device=gpu, dtype=torch.int32) % 1021).to(torch.float16).view(1, half)
+    assert torch.equal(capi.cat([a, b], 1), torch.cat([a, b], 1))
+    del a, b
+    torch.cuda.empty_cache()
