@@ -240,6 +240,15 @@ def op_maxpool(capi, dev, n, rotate=True):
     return (lambda st: capi.maxpool_nc1hwc0(st[0], 5, out=st[1])), sets, algo
 
 
+def op_sppf(capi, dev, n, rotate=True):
+    """SPPF pooling + concat on NC1HWC0 [n,256,20,20]: cat([x, p(x), p(p(x)),
+    p(p(p(x)))], 1), p the k5 pool, in one pass (x read once, 4 slots written)."""
+    algo = n * 16 * 20 * 20 * 16 * 2 * 5
+    sets = rotated(lambda i: (blocked_normal(n, 256, 20, 20, 230 + i, dev),
+                              torch.empty((n, 64, 20, 20, 16), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.sppf_nc1hwc0(st[0], 5, 3, out=st[1])), sets, algo
+
+
 def op_decode(capi, dev, n, rotate=True):
     """Anchor-free head decode: DFL [n,64,8400] + sigmoid [n,80,8400] -> [n,84,8400]."""
     a = 8400
@@ -293,6 +302,7 @@ def op_rows(capi, dev):
         rows.append(("sigmoid_80x8400", "C4", n, lambda r, n=n: op_sigmoid(capi, dev, n, r)))
         rows.append(("softmax_4x400x400", "C5", n, lambda r, n=n: op_softmax(capi, dev, n, r)))
         rows.append(("maxpool_k5_256x20x20", "SPPF", n, lambda r, n=n: op_maxpool(capi, dev, n, r)))
+        rows.append(("sppf_k5x3_cat_256x20x20", "SPPF", n, lambda r, n=n: op_sppf(capi, dev, n, r)))
         rows.append(("detect_decode_64+80x8400", "C4", n, lambda r, n=n: op_decode(capi, dev, n, r)))
         rows.append(("permute_nchw_to_nhwc_64x80x80", "MAT", n, lambda r, n=n: op_permute(capi, dev, n, r)))
     for layout in ("contiguous", "transposed"):
@@ -346,6 +356,15 @@ def cpu_op(name, n):
     if name == "maxpool_k5_256x20x20":
         x = h16(n, 256, 20, 20)
         return (lambda: F.max_pool2d(x.float(), 5, 1, 2).half()), x.numel() * 4
+    if name == "sppf_k5x3_cat_256x20x20":
+        x = h16(n, 256, 20, 20)
+
+        def sppf():
+            ys = [x]
+            for _ in range(3):
+                ys.append(F.max_pool2d(ys[-1].float(), 5, 1, 2).half())
+            return torch.cat(ys, 1)
+        return sppf, x.numel() * 2 * 5
     if name == "detect_decode_64+80x8400":
         from oracle import detect as dt  # the CPU decode sequence, timed
         b, sc = h16(n, 64, 8400) * 3, h16(n, 80, 8400)

@@ -168,6 +168,16 @@ thin_status thin_unpack_nc1hwc0(const thin_desc* x, const thin_desc* y, hipStrea
  * maxpool_tiles (flow_ops.cpp:82-127,208-231; SPPF k5). */
 thin_status thin_maxpool_nc1hwc0(const thin_desc* x, int32_t kernel, const thin_desc* out, hipStream_t stream);
 
+/* SPPF pooling and concat in one pass: out = cat([x, p(x), p(p(x)), ...], dim 1)
+ * with p the max pool above (odd kernel in [1, 15]) applied `repeats` times
+ * (1..8), each repeat pooling the previous one's output, so +0/-0 ties and
+ * NaNs come out as from chained thin_maxpool_nc1hwc0 calls.  fp16 NC1HWC0:
+ * x [N,C1,H,W,16], out [N,(repeats+1)*C1,H,W,16], strides as for the pool.
+ * Replaces the SPPF block's three k5 pools (whole_blocked.py:63-64,259-262,
+ * flow_ops.cpp:82-127) and the cat of their outputs (ops.cpp:419-462). */
+thin_status thin_sppf_nc1hwc0(const thin_desc* x, int32_t kernel, int32_t repeats, const thin_desc* out,
+                              hipStream_t stream);
+
 /* The same pool over NCHW fp16/fp32, any strides.  Replaces thin::maxpool2d
  * (backend.cpp:245-266; maxpool.cpp:1-60, k5 s1 p2) and serves aten
  * max_pool2d_with_indices (aten_adapter.cpp:61-80). */

@@ -93,3 +93,14 @@ def maxpool_blocked(x: torch.Tensor, kernel: int) -> torch.Tensor:
     nchw = x.permute(0, 1, 4, 2, 3).reshape(n, c1 * c0, h, w)
     y = maxpool_nchw(nchw, kernel)
     return y.reshape(n, c1, c0, h, w).permute(0, 1, 3, 4, 2).contiguous()
+
+
+def sppf_blocked(x: torch.Tensor, kernel: int = 5, repeats: int = 3) -> torch.Tensor:
+    """The SPPF block's pooling and concat (Ultralytics SPPF.forward, whose
+    pools the reference runs through maxpool_forward, whole_blocked.py:63-64,
+    and whose cat is thin_ops::cat, ops.cpp:419-462): each pool takes the
+    previous one's output, cat over C1."""
+    ys = [x]
+    for _ in range(repeats):
+        ys.append(maxpool_blocked(ys[-1], kernel))
+    return torch.cat(ys, 1)

@@ -131,7 +131,7 @@ def test_glue_registers_privateuse1():
                "aten::as_strided", "aten::view", "aten::split.Tensor", "aten::convolution",
                "thin_backend::add", "thin_backend::sigmoid", "thin_backend::upsample_nearest2d",
                "thin_fused::silu_add", "thin_fused::affine_silu", "thin_fused::upsample_cat",
-               "thin_fused::dfl_expect", "thin_fused::detect_decode", "thin_native_flow::upsample",
+               "thin_fused::dfl_expect", "thin_fused::detect_decode", "thin_fused::sppf", "thin_native_flow::upsample",
                "thin_native_flow::pack_input", "thin_native_flow::maxpool", "thin_backend::maxpool2d",
                "aten::max_pool2d_with_indices", "aten::fill_.Scalar", "aten::zero_",
                "thin_native_flow::detection_select", "thin_native_flow::detection_select_trace",
@@ -163,6 +163,8 @@ def test_fused_meta_shapes():
     b = torch.empty(2, 64, 21, dtype=torch.float16, device="meta")
     sc = torch.empty(2, 3, 21, dtype=torch.float16, device="meta")
     assert torch.ops.thin_fused.detect_decode(b, sc, [3, 5, 2, 3], [8.0, 16.0]).shape == (2, 7, 21)
+    assert torch.ops.thin_fused.sppf(x).shape == (2, 16, 8, 8, 16)
+    assert torch.ops.thin_fused.sppf(x, 3, 1).shape == (2, 8, 8, 8, 16)
 
 
 def test_no_cpu_fallback_without_library(monkeypatch, tmp_path):

@@ -290,6 +290,14 @@ def test_flow_ops(npu):
         assert bits_equal(torch.ops.thin_native_flow.maxpool(ym, 5).cpu(), mv.maxpool_blocked(mv.pack_blocked(xm), 5))
         with pytest.raises(RuntimeError, match="odd"):
             torch.ops.thin_native_flow.maxpool(ym, 4)
+        # the SPPF block's three pools and concat as one op (cv2's input)
+        assert bits_equal(torch.ops.thin_fused.sppf(ym).cpu(), mv.sppf_blocked(mv.pack_blocked(xm), 5, 3))
+        pools = [ym]
+        for _ in range(3):
+            pools.append(torch.ops.thin_native_flow.maxpool(pools[-1], 5))
+        assert bits_equal(torch.ops.thin_fused.sppf(ym, 5, 3).cpu(), torch.cat(pools, 1).cpu())
+        with pytest.raises(RuntimeError, match="repeats"):
+            torch.ops.thin_fused.sppf(ym, 5, 0)
 
 
 def test_fused_ops(npu):

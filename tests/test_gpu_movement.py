@@ -322,3 +322,46 @@ def test_cat_beyond_4gib(gpu):
     assert torch.equal(capi.cat([a, b], 1), torch.cat([a, b], 1))
     del a, b
     torch.cuda.empty_cache()
+
+
+SPPF_SHAPES = [(256, 20, 20, 5, 3), (32, 13, 17, 3, 2), (16, 7, 9, 7, 1), (32, 9, 11, 1, 3), (16, 5, 6, 15, 4)]
+
+
+@pytest.mark.parametrize("n", [1, 2])
+def test_sppf_chain(gpu, n):
+    """thin_sppf_nc1hwc0 = cat([x, p(x), p(p(x)), ...], 1): bit-exact against
+    chained oracle pools (+0/-0 ties through the first-maximum path, special
+    values through the packed path)."""
+    from thintnpu_amd import capi
+    for c, h, w, k, r in SPPF_SHAPES:
+        x = to_blocked(normal16((n, c, h, w), c + h + k))
+        check_pool(capi.sppf_nc1hwc0(x.to(gpu), k, r).cpu(), mv.sppf_blocked(x, k, r), f"{c}x{h}x{w} k{k} r{r}")
+    x = pool_specials(to_blocked(normal16((n, 32, 9, 11), 6)))
+    for k in (3, 5, 7):
+        check_pool(capi.sppf_nc1hwc0(x.to(gpu), k, 3).cpu(), mv.sppf_blocked(x, k, 3), f"specials k{k}")
+    for zero in (None, 0.0, -0.0):
+        x = pool_specials_packed(to_blocked(normal16((n, 64, 20, 20), 32)), zero, 43)
+        check_pool(capi.sppf_nc1hwc0(x.to(gpu), 5, 3).cpu(), mv.sppf_blocked(x, 5, 3), f"packed zero={zero}")
+
+
+def test_sppf_large_planes_and_views(gpu):
+    """A 40x40 plane (118 KB of LDS per block), a 64x64 plane (beyond one
+    block's LDS: copy plus chained pools), a channel-block slice as x, and an
+    output that is a slice of a larger tensor."""
+    from thintnpu_amd import capi
+    for c, h, w in ((32, 40, 40), (16, 64, 64)):
+        x = pool_specials(to_blocked(normal16((2, c, h, w), h)))
+        check_pool(capi.sppf_nc1hwc0(x.to(gpu), 5, 3).cpu(), mv.sppf_blocked(x, 5, 3), f"{c}x{h}x{w}")
+    x = to_blocked(normal16((2, 64, 12, 10), 9))
+    xd = x.to(gpu)
+    check_pool(capi.sppf_nc1hwc0(xd[:, 1:3], 5, 3).cpu(), mv.sppf_blocked(x[:, 1:3].contiguous(), 5, 3), "x slice")
+    parent = random_bits16((2, 12, 12, 10, 16), 10)
+    pd = parent.to(gpu)
+    capi.sppf_nc1hwc0(xd[:, :2], 3, 2, out=pd[:, 5:11])
+    got = pd.cpu()
+    check_pool(got[:, 5:11], mv.sppf_blocked(x[:, :2].contiguous(), 3, 2), "out slice")
+    assert bits_equal(got[:, :5], parent[:, :5]) and bits_equal(got[:, 11:], parent[:, 11:])
+    with pytest.raises(capi.ThinError, match="repeats"):
+        capi.sppf_nc1hwc0(xd[:, :2], 5, 0, out=torch.empty((2, 2, 12, 10, 16), dtype=torch.float16, device=gpu))
+    with pytest.raises(capi.ThinError, match="out must be"):
+        capi.sppf_nc1hwc0(xd[:, :2], 5, 3, out=torch.empty((2, 6, 12, 10, 16), dtype=torch.float16, device=gpu))

@@ -109,3 +109,23 @@ def test_maxpool_against_brute_force(k):
     blocked = to_blocked(torch.cat((x, x.flip(1), x, x.flip(2), x, x), 1)[:, :16])
     assert bits_equal(mv.maxpool_blocked(blocked, k),
                       to_blocked(mv.maxpool_nchw(torch.cat((x, x.flip(1), x, x.flip(2), x, x), 1)[:, :16], k)))
+
+
+def test_sppf_chain_identities():
+    """sppf_blocked: slot 0 is x; with no +0/-0 ties the r-th chained k-pool is
+    one (r*(k-1)+1)-wide pool (max over a window of windows, -inf padding never
+    wins), which a slot pooling x instead of its predecessor would fail; a NaN
+    spreads by k//2 pixels per repeat."""
+    g = torch.Generator().manual_seed(5)
+    x = to_blocked(torch.randn(2, 32, 9, 11, generator=g).half())
+    for k in (3, 5):
+        y = mv.sppf_blocked(x, k, 3)
+        assert y.shape == (2, 8, 9, 11, 16)
+        assert bits_equal(y[:, :2], x)
+        for r in (1, 2, 3):
+            assert bits_equal(y[:, 2 * r:2 * r + 2], mv.maxpool_blocked(x, r * (k - 1) + 1)), (k, r)
+    z = x.clone()
+    z[0, 0, 4, 5, 3] = float("nan")
+    y = mv.sppf_blocked(z, 5, 2)
+    rows, cols = torch.nonzero(torch.isnan(y[0, 4, :, :, 3]), as_tuple=True)
+    assert (rows.min(), rows.max(), cols.min(), cols.max()) == (0, 8, 1, 9)

@@ -82,6 +82,7 @@ def lib() -> ctypes.CDLL:
             "thin_softmax": [P, i32, P, vp],
             "thin_dfl_expect": [P, P, vp],
             "thin_maxpool_nc1hwc0": [P, i32, P, vp],
+            "thin_sppf_nc1hwc0": [P, i32, i32, P, vp],
             "thin_maxpool2d_nchw": [P, i32, P, vp],
             "thin_fill": [P, f64, i64, vp],
             "thin_detect_decode": [P, P, ctypes.POINTER(i32), ctypes.POINTER(f64), i32, i32, P, vp],
@@ -252,6 +253,15 @@ def maxpool_nc1hwc0(x, kernel: int, out=None, stream=None):
     """Stride-1 k x k max pool with padding k//2 on NC1HWC0 fp16."""
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
     _call("thin_maxpool_nc1hwc0", _ref(desc(x)), kernel, _ref(desc(out)), _stream(stream))
+    return out
+
+
+def sppf_nc1hwc0(x, kernel: int = 5, repeats: int = 3, out=None, stream=None):
+    """cat([x, p(x), p(p(x)), ...], 1) with p the stride-1 k x k max pool, on
+    NC1HWC0 fp16 (the SPPF block's pooling and concat)."""
+    n, c1, h, w, c0 = x.shape
+    out = torch.empty((n, (repeats + 1) * c1, h, w, c0), dtype=x.dtype, device=x.device) if out is None else out
+    _call("thin_sppf_nc1hwc0", _ref(desc(x)), kernel, repeats, _ref(desc(out)), _stream(stream))
     return out
 
 

@@ -421,6 +421,27 @@ at::Tensor detect_decode(const at::Tensor& boxes, const at::Tensor& scores, at::
   return out;
 }
 
+// SPPF pooling and concat: cat([x, p(x), p(p(x)), ...], 1), p the stride-1
+// k x k max pool, NC1HWC0 fp16.
+std::vector<int64_t> sppf_sizes(const at::Tensor& x, int64_t kernel, int64_t repeats) {
+  TORCH_CHECK(x.scalar_type() == at::kHalf && x.dim() == 5 && x.size(4) == 16,
+              "sppf expects float16 NC1HWC0 [N,C1,H,W,16]");
+  TORCH_CHECK(kernel >= 1 && kernel <= 15 && kernel % 2 == 1 && repeats >= 1 && repeats <= 8,
+              "sppf takes an odd kernel in [1, 15] and 1..8 repeats");
+  return {x.size(0), (repeats + 1) * x.size(1), x.size(2), x.size(3), 16};
+}
+at::Tensor sppf(const at::Tensor& x, int64_t kernel, int64_t repeats) {
+  inference(x, "thin_fused.sppf");
+  auto sizes = sppf_sizes(x, kernel, repeats);
+  select(x.device());
+  auto out = at::empty(sizes, x.options());
+  if (!out.numel()) return out;
+  thin_desc xd = desc(x), od = desc(out);
+  check(thin_sppf_nc1hwc0(&xd, (int32_t)kernel, (int32_t)repeats, &od, stream()), "thin sppf");
+  after_launch();
+  return out;
+}
+
 // Meta kernels of thin_fused: the shapes and dtypes of the device kernels.
 at::Tensor silu_add_meta(const at::Tensor& x, const at::Tensor& y) {
   TORCH_CHECK(float_type(x) && x.scalar_type() == y.scalar_type(), "silu_add requires matching float16/float32");
@@ -438,6 +459,9 @@ at::Tensor detect_decode_meta(const at::Tensor& boxes, const at::Tensor& scores,
                               at::ArrayRef<double> strides, bool) {
   decode_check(boxes, scores, shapes, strides);
   return at::empty({boxes.size(0), 4 + scores.size(1), boxes.size(2)}, boxes.options());
+}
+at::Tensor sppf_meta(const at::Tensor& x, int64_t kernel, int64_t repeats) {
+  return at::empty(sppf_sizes(x, kernel, repeats), x.options());
 }
 at::Tensor dfl_expect_meta(const at::Tensor& x, bool fp32_output) {
   TORCH_CHECK(x.scalar_type() == at::kHalf && x.dim() == 3 && x.size(1) == 64,
@@ -494,6 +518,7 @@ TORCH_LIBRARY(thin_fused, m) {
   m.def("upsample_cat(Tensor[] tensors, int[] upsample) -> Tensor");
   m.def("dfl_expect(Tensor x, bool fp32_output=False) -> Tensor");
   m.def("detect_decode(Tensor boxes, Tensor scores, int[] shapes, float[] strides, bool xywh=False) -> Tensor");
+  m.def("sppf(Tensor x, int kernel=5, int repeats=3) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(thin_fused, PrivateUse1, m) {
@@ -502,10 +527,11 @@ TORCH_LIBRARY_IMPL(thin_fused, PrivateUse1, m) {
   m.impl("upsample_cat", TORCH_FN(thin_ops::upsample_cat));
   m.impl("dfl_expect", TORCH_FN(thin_ops::dfl_expect));
   m.impl("detect_decode", TORCH_FN(thin_ops::detect_decode));
+  m.impl("sppf", TORCH_FN(thin_ops::sppf));
 }
 
 TORCH_LIBRARY_IMPL(thin_fused, AutogradPrivateUse1, m) {
-  for (const char* name : {"silu_add", "affine_silu", "upsample_cat", "dfl_expect", "detect_decode"})
+  for (const char* name : {"silu_add", "affine_silu", "upsample_cat", "dfl_expect", "detect_decode", "sppf"})
     m.impl(name, torch::CppFunction::makeFallthrough());
 }
 
@@ -515,4 +541,5 @@ TORCH_LIBRARY_IMPL(thin_fused, Meta, m) {
   m.impl("upsample_cat", TORCH_FN(thin_ops::upsample_cat_meta));
   m.impl("dfl_expect", TORCH_FN(thin_ops::dfl_expect_meta));
   m.impl("detect_decode", TORCH_FN(thin_ops::detect_decode_meta));
+  m.impl("sppf", TORCH_FN(thin_ops::sppf_meta));
 }
