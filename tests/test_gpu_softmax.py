@@ -197,3 +197,19 @@ def test_class_sigmoid_c4(gpu, n):
     from thintnpu_amd import capi
     x = normal16((n, 80, 8400), 14, mean=-4.0, std=2.0)
     assert_ulp(capi.unary(capi.SIGMOID, x.to(gpu)).cpu(), ew.sigmoid(x), 2, f"sigmoid n={n}")
+
+
+def test_softmax_row_widths(gpu):
+    """fp16 rows whose 16-byte chunk count is not a power of two (idle lanes
+    in the last chunk round), row counts that leave a partial last block, and
+    rows with NaN, +inf, all -inf, -inf mixed in and large shifts."""
+    from thintnpu_amd import capi
+    for rows, width in ((100, 400), (7, 120), (33, 2040), (41, 136)):
+        x = normal16((rows, width), rows + width, std=3.0)
+        x[0, 5] = float("nan")
+        x[1, 7] = float("inf")
+        x[2] = float("-inf")
+        x[3, ::3] = float("-inf")
+        x[4] += 10000
+        x[5] -= 10000
+        check_softmax(run(capi, x.to(gpu), 1), x, 1, what=f"tiles {rows}x{width}")
