@@ -240,6 +240,18 @@ def op_maxpool(capi, dev, n, rotate=True):
     return (lambda st: capi.maxpool_nc1hwc0(st[0], 5, out=st[1])), sets, algo
 
 
+def op_dfl_softmax(capi, dev, n, rotate=True):
+    """The DFL bin softmax as the reference's aten path computes it
+    (softmax_host.cpp:29-50): softmax over dim 1 of x.view(n,4,16,A).transpose(1,2)
+    for logits [n,64,8400], written to a contiguous [n,16,4,8400]."""
+    a = 8400
+    algo = n * 64 * a * 2 * 2
+    g = torch.Generator(device=dev).manual_seed(9)
+    sets = rotated(lambda i: ((torch.randn((n, 64, a), generator=g, device=dev) * 3).half(),
+                              torch.empty((n, 16, 4, a), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.softmax(st[0].view(n, 4, 16, a).transpose(1, 2), 1, out=st[1])), sets, algo
+
+
 def op_sppf(capi, dev, n, rotate=True):
     """SPPF pooling + concat on NC1HWC0 [n,256,20,20]: cat([x, p(x), p(p(x)),
     p(p(p(x)))], 1), p the k5 pool, in one pass (x read once, 4 slots written)."""
@@ -300,6 +312,7 @@ def op_rows(capi, dev):
         rows.append(("upsample_cat_256+128", "C3", n, lambda r, n=n: op_upsample_cat(capi, dev, n, r)))
         rows.append(("dfl_expect_64x8400", "C4", n, lambda r, n=n: op_dfl(capi, dev, n, r)))
         rows.append(("sigmoid_80x8400", "C4", n, lambda r, n=n: op_sigmoid(capi, dev, n, r)))
+        rows.append(("dfl_softmax_16x4x8400", "C4", n, lambda r, n=n: op_dfl_softmax(capi, dev, n, r)))
         rows.append(("softmax_4x400x400", "C5", n, lambda r, n=n: op_softmax(capi, dev, n, r)))
         rows.append(("maxpool_k5_256x20x20", "SPPF", n, lambda r, n=n: op_maxpool(capi, dev, n, r)))
         rows.append(("sppf_k5x3_cat_256x20x20", "SPPF", n, lambda r, n=n: op_sppf(capi, dev, n, r)))
@@ -347,6 +360,9 @@ def cpu_op(name, n):
         w = torch.arange(16, dtype=torch.float32).view(1, 1, 16, 1)
         return (lambda: (torch.softmax(x.float().view(n, 4, 16, 8400), 2) * w).sum(2).half()), \
             n * (64 + 4) * 8400 * 2
+    if name == "dfl_softmax_16x4x8400":
+        x = h16(n, 64, 8400) * 3
+        return (lambda: torch.softmax(x.view(n, 4, 16, 8400).transpose(1, 2), 1)), x.numel() * 4
     if name == "sigmoid_80x8400":
         x = h16(n, 80, 8400)
         return (lambda: torch.sigmoid(x)), x.numel() * 4

@@ -198,23 +198,52 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
     s[j] = 0.f;
   }
   if (p.R <= (uint32_t)RREG) {
+    // rows past R re-read row R - 1 (unconditional loads keep every row in
+    // flight) and are masked out below
     WI reg[RREG];
 #pragma unroll
+    for (int r = 0; r < RREG; ++r)
+      reg[r] = *reinterpret_cast<const WI*>(xc + (int64_t)min((uint32_t)r, p.R - 1) * p.xr);
+#pragma unroll
     for (int r = 0; r < RREG; ++r) {
-      if (r >= (int)p.R) continue;
-      reg[r] = *reinterpret_cast<const WI*>(xc + r * p.xr);
+      if (r >= (int)p.R) break;
 #pragma unroll
       for (int j = 0; j < V; ++j) m[j] = max_nan(m[j], (float)reg[r].e[j]);
     }
+    if constexpr (V * RREG <= 32) {
+      // few columns per thread: each exponential once, kept in registers;
+      // fp16 outputs take e * (1/s), fp32 outputs e / s
+      float e[RREG][V];
+#pragma unroll
+      for (int r = 0; r < RREG; ++r) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          e[r][j] = r < (int)p.R ? expo<FAST>((float)reg[r].e[j] - m[j]) : 0.f;
+          s[j] += e[r][j];
+        }
+      }
+      float inv[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) inv[j] = 1.0f / s[j];
+#pragma unroll
+      for (int r = 0; r < RREG; ++r) {
+        if (r >= (int)p.R) break;
+        WO w;
+#pragma unroll
+        for (int j = 0; j < V; ++j) w.e[j] = (TO)(FAST ? e[r][j] * inv[j] : e[r][j] / s[j]);
+        *reinterpret_cast<WO*>(oc + r * p.orr) = w;
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < RREG; ++r) {
-      if (r >= (int)p.R) continue;
+      if (r >= (int)p.R) break;
 #pragma unroll
       for (int j = 0; j < V; ++j) s[j] += expo<FAST>((float)reg[r].e[j] - m[j]);
     }
 #pragma unroll
     for (int r = 0; r < RREG; ++r) {
-      if (r >= (int)p.R) continue;
+      if (r >= (int)p.R) break;
       WO w;
 #pragma unroll
       for (int j = 0; j < V; ++j) w.e[j] = (TO)(expo<FAST>((float)reg[r].e[j] - m[j]) / s[j]);
@@ -511,7 +540,17 @@ thin_status launch_softmax(const thin_desc* x, int dim, const thin_desc* out, hi
              (p.xr * (int64_t)sizeof(TI)) % 16 == 0 && (p.orr * (int64_t)sizeof(TO)) % (V * sizeof(TO) >= 16 ? 16 : 1) == 0;
   for (int i = 1; vec && i < p.nd; ++i)
     vec = (p.xs[i] * (int64_t)sizeof(TI)) % 16 == 0 && (p.os[i] * (int64_t)sizeof(TO)) % 16 == 0;
-  if (vec) {
+  // short fp16 columns (the DFL bin softmax over [B,16,4,A], R = 16): two
+  // columns per thread keep every exponential in registers and many waves in
+  // flight ([32,16,4,8400]: 37 us with eight columns per thread)
+  bool pair = sizeof(TI) == 2 && R <= 16 && p.nd >= 1 && p.xs[0] == 1 && p.os[0] == 1 && p.size[0] % 2 == 0 &&
+              aligned(x->data, 4) && aligned(out->data, 2 * sizeof(TO)) && p.xr % 2 == 0 && p.orr % 2 == 0;
+  for (int i = 1; pair && i < p.nd; ++i) pair = p.xs[i] % 2 == 0 && p.os[i] % 2 == 0;
+  if (pair) {
+    p.units = (uint32_t)(cols / 2);
+    const uint32_t grid = (p.units + kThreads - 1) / kThreads;
+    hipLaunchKernelGGL((softmax_col_kernel<TI, TO, 2, 16, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
+  } else if (vec) {
     p.units = (uint32_t)(cols / V);
     const uint32_t grid = (p.units + kThreads - 1) / kThreads;
     hipLaunchKernelGGL((softmax_col_kernel<TI, TO, V, 16, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
