@@ -213,3 +213,26 @@ def test_softmax_row_widths(gpu):
         x[4] += 10000
         x[5] -= 10000
         check_softmax(run(capi, x.to(gpu), 1), x, 1, what=f"tiles {rows}x{width}")
+
+
+def test_softmax_short_columns(gpu):
+    """Reductions of <= 16 rows whose columns run contiguous in the innermost
+    dim (the DFL bin softmax layout), staged through LDS tiles: reductions
+    shorter than 16, a partial last tile of innermost columns (136 = 128 + 8),
+    outer column counts that leave a partial group, NaN / +inf / all -inf
+    columns, and the transposed DFL view itself."""
+    from thintnpu_amd import capi
+    for shape in ((3, 5, 3, 136), (2, 16, 4, 64), (1, 1, 2, 8), (2, 9, 1, 256)):
+        x = normal16(shape, sum(shape), std=3.0)
+        x[0, 0, 0, 3] = float("nan")
+        x[0, :, 0, 5] = float("-inf")
+        x[-1, -1, -1, 7] = float("inf")
+        x[0, 0, -1, 1] += 10000
+        check_softmax(run(capi, x.to(gpu), 1), x, 1, what=f"short columns {shape}")
+    a = 8400
+    logits = normal16((2, 64, a), 3, std=3.0)
+    logits[0, 17, 9] = float("nan")
+    logits[1, 32:48, 100] = float("-inf")
+    view = logits.view(2, 4, 16, a).transpose(1, 2)
+    got = capi.softmax(logits.to(gpu).view(2, 4, 16, a).transpose(1, 2), 1).cpu()
+    check_softmax(got, view, 1, what="DFL bin view")
