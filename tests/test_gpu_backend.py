@@ -477,3 +477,19 @@ def test_decode_constants(npu):
         x = torch.arange(12, device="npu", dtype=torch.float32).view(3, 4)
         torch.testing.assert_close(torch.stack(torch.unbind(x)).cpu(), torch.arange(12, dtype=torch.float32).view(3, 4))
         assert torch.full((), 8.0, device="npu").item() == 8.0
+
+
+def test_reference_permute_sites(npu):
+    """The reference's .contiguous()-after-permute call sites on npu tensors --
+    the anchor head [B,na*no,H,W] -> [B,na,H,W,no] (whole_blocked.py:76) and the
+    NCHW <-> NC1HWC0 repacks around depthwise (model_optimization.py:14,17) --
+    bit-exact; each is a batched 2-D transpose."""
+    with torch.inference_mode():
+        head = normal16((2, 3 * 85, 20, 20), 3)
+        got = head.to(npu).view(2, 3, 85, 20, 20).permute(0, 1, 3, 4, 2).contiguous()
+        assert bits_equal(got.cpu(), head.view(2, 3, 85, 20, 20).permute(0, 1, 3, 4, 2).contiguous())
+        x = normal16((2, 64, 20, 24), 4)
+        blocked = x.to(npu).contiguous().view(2, 4, 16, 20, 24).permute(0, 1, 3, 4, 2).contiguous()
+        assert bits_equal(blocked.cpu(), x.view(2, 4, 16, 20, 24).permute(0, 1, 3, 4, 2).contiguous())
+        back = blocked.permute(0, 1, 4, 2, 3).contiguous().view(2, 64, 20, 24)
+        assert bits_equal(back.cpu(), x)
