@@ -493,3 +493,30 @@ def test_reference_permute_sites(npu):
         assert bits_equal(blocked.cpu(), x.view(2, 4, 16, 20, 24).permute(0, 1, 3, 4, 2).contiguous())
         back = blocked.permute(0, 1, 4, 2, 3).contiguous().view(2, 64, 20, 24)
         assert bits_equal(back.cpu(), x)
+
+
+def test_fused_head_ops_capture(npu):
+    """thin_fused.sppf and thin_fused.detect_decode under CapturedForward
+    (graph.py:14-51): a replay equals eager bitwise, and a call with a new input
+    (copied into the captured one) gives the oracle's result for it."""
+    from thin_backend.graph import CapturedForward
+    with torch.inference_mode():
+        x = to_blocked(normal16((2, 256, 20, 20), 21)).to(npu)
+        graph = CapturedForward(lambda v: torch.ops.thin_fused.sppf(v), x)
+        assert bits_equal(graph.replay().cpu(), torch.ops.thin_fused.sppf(x).cpu())
+        x2 = to_blocked(normal16((2, 256, 20, 20), 22))
+        assert bits_equal(graph(x2.to(npu)).cpu(), mv.sppf_blocked(x2, 5, 3))
+        graph.close()
+        shapes, strides = [8, 8, 4, 4], [8.0, 16.0]
+        boxes, scores = normal16((1, 64, 80), 23, std=3.0), normal16((1, 3, 80), 24)
+        sd = scores.to(npu)
+        forward = lambda b: torch.ops.thin_fused.detect_decode(b, sd, shapes, strides)
+        bd = boxes.to(npu)
+        graph = CapturedForward(forward, bd)
+        assert bits_equal(graph.replay().cpu(), forward(bd).cpu())
+        boxes2 = normal16((1, 64, 80), 25, std=3.0)
+        got = graph(boxes2.to(npu)).cpu()
+        assert bits_equal(got, forward(boxes2.to(npu)).cpu())
+        assert_ulp(got[:, 4:], ew.sigmoid(scores), 2)
+        assert torch.isfinite(got).all() and got[:, :4].abs().sum() > 0
+        graph.close()
