@@ -772,6 +772,46 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(TransposePlan p) {
   const T* src = reinterpret_cast<const T*>(p.src) + b * p.s_b;
   T* dst = reinterpret_cast<T*>(p.dst) + b * p.d_b;
   const bool full = m0 + kTile <= p.M && p0 + kTile <= p.P;
+  if constexpr (sizeof(T) == 2) {
+    if (full && p.vec_src && p.vec_dst) {
+      // whole 2-byte tiles with 16-byte rows on both sides: every load in
+      // flight before the LDS writes (4-byte words), and each thread reads
+      // 4-byte column pairs from 8 tile rows to build two output vectors
+      typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+      constexpr uint32_t U = kTile * kTile / V / kThreads;  // 2
+      constexpr uint32_t kWords = kRow / 2;                 // padded row in 4-byte words (33)
+      uint32_t* words = reinterpret_cast<uint32_t*>(tile);
+      u32x4_t w[U];
+#pragma unroll
+      for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+        w[u] = load16<NT, u32x4_t>(src + (int64_t)(m0 + r) * p.s_m + p0 + cv);
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) words[r * kWords + cv / 2 + k] = w[u][k];
+      }
+      __syncthreads();
+      // thread -> (column pair qp of the tile, 8-row group g): lanes 8 apart
+      // share a destination row, and the 64 lanes hit 64 distinct banks
+      const uint32_t g = threadIdx.x % (kTile / 8), qp = threadIdx.x / (kTile / 8);
+      uint32_t lo[4], hi[4];
+#pragma unroll
+      for (uint32_t j = 0; j < 8; j += 2) {
+        const uint32_t a = words[(g * 8 + j) * kWords + qp], b = words[(g * 8 + j + 1) * kWords + qp];
+        lo[j / 2] = (a & 0xffffu) | (b << 16);           // column 2qp, rows g*8+j, +1
+        hi[j / 2] = (a >> 16) | (b & 0xffff0000u);       // column 2qp+1
+      }
+      T* row0 = dst + (int64_t)(p0 + 2 * qp) * p.d_p + m0 + g * 8;
+      store16<NT>(row0, (u32x4_t){lo[0], lo[1], lo[2], lo[3]});
+      store16<NT>(row0 + p.d_p, (u32x4_t){hi[0], hi[1], hi[2], hi[3]});
+      return;
+    }
+  }
   // load: tile row r = m0 + r, columns p0 .. p0+63
   for (uint32_t i = threadIdx.x; i < kTile * kTile / V; i += kThreads) {
     const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
