@@ -206,9 +206,10 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
       reg[r] = *reinterpret_cast<const WI*>(xc + (int64_t)min((uint32_t)r, p.R - 1) * p.xr);
 #pragma unroll
     for (int r = 0; r < RREG; ++r) {
-      if (r >= (int)p.R) break;
+      if (r < (int)p.R) {
 #pragma unroll
-      for (int j = 0; j < V; ++j) m[j] = max_nan(m[j], (float)reg[r].e[j]);
+        for (int j = 0; j < V; ++j) m[j] = max_nan(m[j], (float)reg[r].e[j]);
+      }
     }
     if constexpr (V * RREG <= 32) {
       // few columns per thread: each exponential once, kept in registers;
@@ -227,27 +228,30 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
       for (int j = 0; j < V; ++j) inv[j] = 1.0f / s[j];
 #pragma unroll
       for (int r = 0; r < RREG; ++r) {
-        if (r >= (int)p.R) break;
-        WO w;
+        if (r < (int)p.R) {
+          WO w;
 #pragma unroll
-        for (int j = 0; j < V; ++j) w.e[j] = (TO)(FAST ? e[r][j] * inv[j] : e[r][j] / s[j]);
-        *reinterpret_cast<WO*>(oc + r * p.orr) = w;
+          for (int j = 0; j < V; ++j) w.e[j] = (TO)(FAST ? e[r][j] * inv[j] : e[r][j] / s[j]);
+          *reinterpret_cast<WO*>(oc + r * p.orr) = w;
+        }
       }
       return;
     }
 #pragma unroll
     for (int r = 0; r < RREG; ++r) {
-      if (r >= (int)p.R) break;
+      if (r < (int)p.R) {
 #pragma unroll
-      for (int j = 0; j < V; ++j) s[j] += expo<FAST>((float)reg[r].e[j] - m[j]);
+        for (int j = 0; j < V; ++j) s[j] += expo<FAST>((float)reg[r].e[j] - m[j]);
+      }
     }
 #pragma unroll
     for (int r = 0; r < RREG; ++r) {
-      if (r >= (int)p.R) break;
-      WO w;
+      if (r < (int)p.R) {
+        WO w;
 #pragma unroll
-      for (int j = 0; j < V; ++j) w.e[j] = (TO)(expo<FAST>((float)reg[r].e[j] - m[j]) / s[j]);
-      *reinterpret_cast<WO*>(oc + r * p.orr) = w;
+        for (int j = 0; j < V; ++j) w.e[j] = (TO)(expo<FAST>((float)reg[r].e[j] - m[j]) / s[j]);
+        *reinterpret_cast<WO*>(oc + r * p.orr) = w;
+      }
     }
     return;
   }
