@@ -281,6 +281,53 @@ def op_permute(capi, dev, n, rotate=True):
     return (lambda st: capi.copy(st[0].permute(0, 2, 3, 1), st[1])), sets, algo
 
 
+# C2PSA attention of YOLO26 at a 640x640 input: 4 heads, key 32, head 64, the
+# 20x20 = 400 tokens of P5, over one N=1 blocked QKV tensor (N=1 only: head
+# groups need an N=1 operand, as in the reference)
+ATTN = (4, 32, 64, 400)
+
+
+def attn_qkv(dev, seed):
+    heads, key, dim, tokens = ATTN
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return torch.randn((1, heads * (2 * key + dim) // 16, tokens, 16), generator=g, device=dev).half()
+
+
+def op_attn_qk(capi, dev, n, rotate=True):
+    """Attention scores per head, q^T k: [400,32] x [32,400] from the grouped
+    blocked QKV (layout_bmm), [4,400,400] fp16 out; 41 MFLOP."""
+    heads, key, dim, tokens = ATTN
+    algo = heads * (2 * key * tokens + tokens * tokens) * 2
+    sets = rotated(lambda i: (attn_qkv(dev, 300 + i),
+                              torch.empty((heads, tokens, tokens), dtype=torch.float16, device=dev)), algo, rotate)
+    return (lambda st: capi.layout_bmm(st[0], st[0], True, False, False, heads, 0, key, key, key, out=st[1])), \
+        sets, algo
+
+
+def op_attn_pv(capi, dev, n, rotate=True):
+    """Attention mix per head, v p^T: [64,400] x [400,400] with the blocked
+    output [1,16,400,16] (layout_bmm, grouped); 82 MFLOP."""
+    heads, key, dim, tokens = ATTN
+    algo = heads * (2 * dim * tokens + tokens * tokens) * 2
+    g = torch.Generator(device=dev).manual_seed(11)
+    sets = rotated(lambda i: (attn_qkv(dev, 310 + i),
+                              torch.rand((heads, tokens, tokens), generator=g, device=dev).half(),
+                              torch.empty((1, heads * dim // 16, tokens, 16), dtype=torch.float16, device=dev)),
+                   algo, rotate)
+    return (lambda st: capi.layout_bmm(st[0], st[1], False, True, True, heads, 2 * key, dim, out=st[2])), \
+        sets, algo
+
+
+def op_attn_select(capi, dev, n, rotate=True):
+    """channel_select of v (the position branch input): [1,16,400,16] out."""
+    heads, key, dim, tokens = ATTN
+    algo = heads * dim * tokens * 2 * 2
+    sets = rotated(lambda i: (attn_qkv(dev, 320 + i),
+                              torch.empty((1, heads * dim // 16, tokens, 16), dtype=torch.float16, device=dev)),
+                   algo, rotate)
+    return (lambda st: capi.channel_select(st[0], heads, 2 * key, dim, out=st[1])), sets, algo
+
+
 def op_select(capi, dev, layout, rotate=False):
     """C5 NMS-free top-300 of [1,8400,84] (latency-bound: report us)."""
     from tests.selection_fixtures import c5_selection_input  # input generator, shared with the tests
@@ -318,6 +365,9 @@ def op_rows(capi, dev):
         rows.append(("sppf_k5x3_cat_256x20x20", "SPPF", n, lambda r, n=n: op_sppf(capi, dev, n, r)))
         rows.append(("detect_decode_64+80x8400", "C4", n, lambda r, n=n: op_decode(capi, dev, n, r)))
         rows.append(("permute_nchw_to_nhwc_64x80x80", "MAT", n, lambda r, n=n: op_permute(capi, dev, n, r)))
+    rows.append(("attn_qk_4x32x400", "ATTN", 1, lambda r: op_attn_qk(capi, dev, 1, r)))
+    rows.append(("attn_pv_4x64x400", "ATTN", 1, lambda r: op_attn_pv(capi, dev, 1, r)))
+    rows.append(("channel_select_4x64x400", "ATTN", 1, lambda r: op_attn_select(capi, dev, 1, r)))
     for layout in ("contiguous", "transposed"):
         rows.append((f"detection_select_{layout}", "C5", 1, lambda r, l=layout: op_select(capi, dev, l)))
     return rows
@@ -389,6 +439,18 @@ def cpu_op(name, n):
     if name == "permute_nchw_to_nhwc_64x80x80":
         x = h16(n, 64, 80, 80)
         return (lambda: x.permute(0, 2, 3, 1).contiguous()), x.numel() * 4
+    if name.startswith("attn_") or name.startswith("channel_select"):
+        from oracle import bmm as ob  # the sequential-fp32 CPU contraction, timed
+        heads, key, dim, tokens = ATTN
+        qkv = h16(1, heads * (2 * key + dim) // 16, tokens, 16)
+        if name.startswith("attn_qk"):
+            return (lambda: ob.layout_bmm(qkv, qkv, True, False, False, heads, 0, key, key, key)), \
+                heads * (2 * key * tokens + tokens * tokens) * 2
+        if name.startswith("attn_pv"):
+            p = torch.rand(heads, tokens, tokens, generator=g).half()
+            return (lambda: ob.layout_bmm(qkv, p, False, True, True, heads, 2 * key, dim)), \
+                heads * (2 * dim * tokens + tokens * tokens) * 2
+        return (lambda: ob.channel_select(qkv, heads, 2 * key, dim)), heads * dim * tokens * 2 * 2
     if name.startswith("detection_select"):
         from oracle import selection as sel  # the stable CPU selection, timed
         from tests.selection_fixtures import c5_selection_input
@@ -483,8 +545,10 @@ def main():
     n = 32
     if args.profile and args.profile.startswith("op:"):
         name, _, nn = args.profile[3:].partition("@")
-        nn = int(nn) if nn else (1 if name.startswith("detection_select") else 32)
-        found = [f for (rname, _, rn, f) in op_rows(capi, dev) if rname == name and rn == nn]
+        rows = [(rn, f) for (rname, _, rn, f) in op_rows(capi, dev) if rname == name]
+        # default: the row's N=32 case, else its only (N=1) case
+        nn = int(nn) if nn else (32 if any(rn == 32 for rn, _ in rows) else 1)
+        found = [f for rn, f in rows if rn == nn]
         if not found:
             print(f"no op row {name!r} at N={nn}", file=sys.stderr)
             sys.exit(2)

@@ -261,6 +261,62 @@ thin_status thin_detection_select(const thin_desc* decoded, int64_t max_det, int
                                   void* out, void* workspace, size_t workspace_bytes,
                                   const thin_select_trace* trace, hipStream_t stream);
 
+/* ------------------------------------------------------------------ */
+/* Attention contractions                                              */
+/* ------------------------------------------------------------------ */
+
+/* Operand interpretation of thin_layout_bmm, the arguments of the reference's
+ * layout_bmm after its two tensors (bmm_flow.cpp:276-278,347).  An operand is
+ * a rank-3 [batch, rows, cols] tensor or a channel-blocked rank-4
+ * [N, C1, T, 16] tensor whose logical matrix has the C1*16 channels as rows
+ * and the T tokens as columns.  groups > 0 splits the channels of an N=1
+ * blocked operand into `groups` heads (the batch); a/b_offset and
+ * a/b_channels select a channel (row) range inside each head, -1 = to the end.
+ * transpose_a/b transpose the logical matrices; blocked_output packs the
+ * [batch, m, n] result as NC1HWC0 [batch, m/16, n, 16], or [1, batch*m/16, n,
+ * 16] when groups > 0. */
+typedef struct thin_bmm_layout {
+  int32_t transpose_a;
+  int32_t transpose_b;
+  int32_t blocked_output;
+  int32_t reserved;
+  int64_t groups;
+  int64_t a_offset;
+  int64_t a_channels;
+  int64_t b_offset;
+  int64_t b_channels;
+} thin_bmm_layout;
+
+/* Validates a layout_bmm call and writes the output's rank and sizes:
+ * [batch, m, n] (the reference allocates n rounded up to 16 columns and
+ * returns the [.., :n] view), or the blocked shape.  Same checks and messages
+ * as dynamic_bmm::run (bmm_flow.cpp:279-312). */
+thin_status thin_layout_bmm_shape(const thin_desc* a, const thin_desc* b, const thin_bmm_layout* layout,
+                                  int32_t* out_rank, int64_t* out_sizes);
+
+/* out = a @ b over the logical fp16 matrices described above; out any
+ * strides, of the shape thin_layout_bmm_shape gives.  Each output is the fp32
+ * sum of its products in reduction order k = 0..K-1 from zero, cast once to
+ * fp16 (round to nearest even): bit-equal to the reference's sequential
+ * accumulation.  Replaces dynamic_bmm::multiply and pack_channels
+ * (bmm_flow.cpp:35-191) behind layout_bmm / bmm / aten::bmm
+ * (bmm_flow.cpp:276-359). */
+thin_status thin_layout_bmm(const thin_desc* a, const thin_desc* b, const thin_bmm_layout* layout,
+                            const thin_desc* out, hipStream_t stream);
+
+/* Output sizes [1, groups*count/16, T, 16] of thin_channel_select, after its
+ * checks (bmm_flow.cpp:255-262). */
+thin_status thin_channel_select_shape(const thin_desc* x, int64_t groups, int64_t begin, int64_t count,
+                                      int64_t* out_sizes);
+
+/* x: fp16 [1, C1, T, 16] (any strides).  Output channel c is input channel
+ * (c / count) * (C1*16 / groups) + begin + c % count: channels
+ * [begin, begin + count) of every one of the `groups` equal channel groups,
+ * packed back to back.  Bit copy.  Replaces channel_select /
+ * channel_select_kernel (bmm_flow.cpp:217-266). */
+thin_status thin_channel_select(const thin_desc* x, int64_t groups, int64_t begin, int64_t count,
+                                const thin_desc* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

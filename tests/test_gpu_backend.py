@@ -129,10 +129,12 @@ def test_aten_routes_and_rejects(npu):
         for name, op in (("conv", lambda: F.conv2d(an, torch.randn(3, 7, 3, 3).to(npu))),
                          ("pool-k3", lambda: F.max_pool2d(an, 3, 1, 1)),
                          ("pool-s2", lambda: F.max_pool2d(an, 5, 2, 2)),
-                         ("nearest-3x", lambda: F.interpolate(an, scale_factor=3, mode="nearest")),
-                         ("bmm", lambda: torch.bmm(an[0], an[0]))):
+                         ("nearest-3x", lambda: F.interpolate(an, scale_factor=3, mode="nearest"))):
             with pytest.raises(RuntimeError, match="thin aten"):
                 op()
+        # aten::bmm is the sequential-fp32 fp16 contraction (bmm_flow.cpp:357-359)
+        with pytest.raises(RuntimeError, match="FP16 rank-3"):
+            torch.bmm(an[0], an[0])
 
 
 def test_thin_backend_namespace(npu):
@@ -520,3 +522,123 @@ def test_fused_head_ops_capture(npu):
         assert_ulp(got[:, 4:], ew.sigmoid(scores), 2)
         assert torch.isfinite(got).all() and got[:, :4].abs().sum() > 0
         graph.close()
+
+
+def test_bmm_flow_eager_and_capture(npu):
+    """verify_bmm_flow.py:14-40: torch.bmm on the device within 0.002 of torch's
+    fp32 bmm and bit-equal to the sequential oracle; a RuntimeGraph replay
+    equals eager, and after new operands are copied in, the replay equals a
+    fresh eager call."""
+    from oracle import bmm as ob
+    g = gen(2026)
+    with torch.inference_mode():
+        for batch, m, k, n in ((4, 400, 32, 400), (4, 64, 400, 400), (2, 17, 9, 23), (3, 5, 37, 1031),
+                               (1, 1, 1, 1)):
+            for transposed in (False, True):
+                a = (torch.randn(batch, k, m, generator=g).transpose(1, 2) if transposed
+                     else torch.randn(batch, m, k, generator=g)).half()
+                b = (torch.randn(batch, n, k, generator=g).transpose(1, 2) if transposed
+                     else torch.randn(batch, k, n, generator=g)).half()
+                left, right = a.to(npu), b.to(npu)
+                actual = torch.bmm(left, right).cpu()
+                torch.testing.assert_close(actual, torch.bmm(a.float(), b.float()).half(), rtol=0.002, atol=0.002)
+                assert bits_equal(actual, ob.sequential_bmm(a, b))
+                graph = torch.classes.thin_backend.RuntimeGraph()
+                graph.begin()
+                captured = torch.bmm(left, right)
+                graph.end()
+                graph.replay()
+                assert bits_equal(captured.cpu(), actual)
+                left.copy_((a * 0.5).to(npu))
+                right.copy_((b * -0.25).to(npu))
+                changed = torch.bmm(left, right).cpu()
+                graph.replay()
+                assert bits_equal(captured.cpu(), changed)
+                graph.close()
+
+
+def test_layout_bmm_and_channel_select_capture(npu):
+    """verify_bmm_layout.py:86-106 through torch.ops.thin_native_flow: grouped
+    q^T k, grouped v p^T with the blocked output and channel_select, each
+    bit-equal to the oracle, to its capture and to a changed-input replay."""
+    from oracle import bmm as ob
+    ops = torch.ops.thin_native_flow
+
+    def check(compute, expect, update):
+        actual = compute().cpu().contiguous()
+        assert bits_equal(actual, expect)
+        graph = torch.classes.thin_backend.RuntimeGraph()
+        graph.begin()
+        captured = compute()
+        graph.end()
+        graph.replay()
+        assert bits_equal(captured.cpu(), actual)
+        update()
+        changed = compute().cpu()
+        graph.replay()
+        assert bits_equal(captured.cpu(), changed)
+        graph.close()
+
+    with torch.no_grad():
+        for heads, key, dim, tokens in ((4, 32, 64, 400), (4, 8, 16, 37), (8, 3, 6, 19)):
+            group = 2 * key + dim
+            logical = torch.randn(heads, group, tokens, generator=gen(heads + key)).half()
+            source = logical.reshape(1, heads * group // 16, 16, tokens).permute(0, 1, 3, 2).contiguous()
+            device = source.to(npu)
+            qr, kr, vr = logical.split((key, key, dim), 1)
+            check(lambda: ops.layout_bmm(device, device, True, False, False, heads, 0, key, key, key),
+                  ob.sequential_bmm(qr.transpose(1, 2), kr), lambda: device.copy_((source * 0.5).to(npu)))
+            device.copy_(source.to(npu))
+            probability = torch.randn(heads, tokens, tokens, generator=gen(7)).half()
+            pd = probability.to(npu)
+            expect = ob.sequential_bmm(vr, probability.transpose(1, 2))
+            expect = expect.reshape(1, heads * dim // 16, 16, tokens).permute(0, 1, 3, 2).contiguous()
+            check(lambda: ops.layout_bmm(device, pd, False, True, True, heads, 2 * key, dim), expect,
+                  lambda: (device.copy_((source * 0.5).to(npu)), pd.copy_((probability * 0.25).to(npu))))
+            device.copy_(source.to(npu))
+            expect = vr.reshape(1, heads * dim // 16, 16, tokens).permute(0, 1, 3, 2).contiguous()
+            check(lambda: ops.channel_select(device, heads, 2 * key, dim), expect,
+                  lambda: device.copy_((source * 0.5).to(npu)))
+        # the unblocked result is the [.., :n] view of 16-column rows
+        a = torch.randn(2, 5, 7, generator=gen(1)).half().to(npu)
+        b = torch.randn(2, 7, 23, generator=gen(2)).half().to(npu)
+        y = ops.bmm(a, b)
+        assert y.shape == (2, 5, 23) and y.stride() == (5 * 32, 32, 1)
+        with pytest.raises(RuntimeError, match="rank-3 operands"):
+            ops.bmm(a.unsqueeze(0), b)
+
+
+def test_attention_block_flow(npu):
+    """The blocked attention forward of whole_blocked.py:91-110 (Q-prescaled
+    order) on the device: channel_select, scale, grouped q^T k, row softmax,
+    grouped v p^T with the blocked output, channel_select of v, add.  Each step
+    is checked against the oracle applied to the device's own input to that
+    step: exact everywhere except the softmax (1e-3 relative)."""
+    from oracle import bmm as ob
+    ops = torch.ops.thin_native_flow
+    batch, num_heads, key_dim, head_dim, h, w = 1, 4, 32, 64, 20, 20
+    tokens, heads = h * w, batch * num_heads
+    scale = key_dim ** -0.5
+    channels = num_heads * (2 * key_dim + head_dim)
+    qkv_blocked = to_blocked(normal16((batch, channels, h, w), 31))          # [1, C1, h, w, 16]
+    with torch.no_grad():
+        qkv = qkv_blocked.to(npu).view(batch, -1, tokens, 16)
+        selected = ops.channel_select(qkv, heads, 0, key_dim)
+        query = selected * scale
+        scores = ops.layout_bmm(query, qkv, True, False, False, heads, 0, key_dim, key_dim, key_dim)
+        probability = scores.softmax(dim=-1)
+        mixed = ops.layout_bmm(qkv, probability, False, True, True, heads, 2 * key_dim, head_dim)
+        mixed = mixed.view(batch, num_heads * head_dim // 16, h, w, 16)
+        position = ops.channel_select(qkv, heads, 2 * key_dim, head_dim).view(batch, -1, h, w, 16)
+        out = mixed + position
+    q_cpu = qkv_blocked.view(batch, -1, tokens, 16)
+    assert bits_equal(selected.cpu(), ob.channel_select(q_cpu, heads, 0, key_dim))
+    assert bits_equal(query.cpu(), ew.binary_scalar(1, selected.cpu(), scale))
+    assert scores.shape == (heads, tokens, tokens)
+    assert bits_equal(scores.cpu(), ob.layout_bmm(query.cpu(), q_cpu, True, False, False, heads, 0, key_dim,
+                                                  key_dim, key_dim))
+    assert_rel(probability.cpu(), rd.softmax(scores.cpu(), -1), 1e-3)
+    expect = ob.layout_bmm(q_cpu, probability.cpu(), False, True, True, heads, 2 * key_dim, head_dim)
+    assert bits_equal(mixed.cpu(), expect.view(batch, -1, h, w, 16))
+    assert bits_equal(position.cpu(), ob.channel_select(q_cpu, heads, 2 * key_dim, head_dim).view(batch, -1, h, w, 16))
+    assert bits_equal(out.cpu(), ew.binary(3, mixed.cpu(), position.cpu()))

@@ -47,6 +47,13 @@ class ThinSelectTrace(ctypes.Structure):
                 ("class_max", "stage1", "gathered", "top_values", "stage2", "anchors", "labels")]
 
 
+class ThinBmmLayout(ctypes.Structure):
+    _fields_ = [("transpose_a", ctypes.c_int32), ("transpose_b", ctypes.c_int32),
+                ("blocked_output", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("groups", ctypes.c_int64), ("a_offset", ctypes.c_int64), ("a_channels", ctypes.c_int64),
+                ("b_offset", ctypes.c_int64), ("b_channels", ctypes.c_int64)]
+
+
 class ThinError(RuntimeError):
     """A C-ABI call returned a non-zero thin_status."""
 
@@ -88,6 +95,11 @@ def lib() -> ctypes.CDLL:
             "thin_detect_decode": [P, P, ctypes.POINTER(i32), ctypes.POINTER(f64), i32, i32, P, vp],
             "thin_detection_select": [P, i64, i32, vp, vp, ctypes.c_size_t,
                                       ctypes.POINTER(ThinSelectTrace), vp],
+            "thin_layout_bmm_shape": [P, P, ctypes.POINTER(ThinBmmLayout), ctypes.POINTER(i32),
+                                      ctypes.POINTER(i64)],
+            "thin_layout_bmm": [P, P, ctypes.POINTER(ThinBmmLayout), P, vp],
+            "thin_channel_select_shape": [P, i64, i64, i64, ctypes.POINTER(i64)],
+            "thin_channel_select": [P, i64, i64, i64, P, vp],
         }
         for name, argtypes in sigs.items():
             fn = getattr(L, name, None)
@@ -339,4 +351,43 @@ def detection_select(decoded, max_det: int, agnostic: bool = False, trace: bool 
           ctypes.byref(tr) if tr is not None else None, _stream(stream))
     if trace:
         return out, tensors
+    return out
+
+
+def layout_bmm(a, b, transpose_a: bool = False, transpose_b: bool = False, blocked_output: bool = False,
+               groups: int = 0, a_offset: int = 0, a_channels: int = -1, b_offset: int = 0, b_channels: int = -1,
+               out=None, stream=None):
+    """a @ b over the logical fp16 matrices of rank-3 or channel-blocked
+    rank-4 operands (head groups, channel ranges, transposes), summed in fp32
+    in reduction order.  Unblocked results are the [.., :n] view of a buffer
+    whose rows are n rounded up to 16 columns, as the reference returns them."""
+    L = ThinBmmLayout(int(transpose_a), int(transpose_b), int(blocked_output), 0, groups, a_offset, a_channels,
+                      b_offset, b_channels)
+    rank = ctypes.c_int32()
+    sizes = (ctypes.c_int64 * 4)()
+    _call("thin_layout_bmm_shape", _ref(desc(a)), _ref(desc(b)), ctypes.byref(L), ctypes.byref(rank), sizes)
+    shape = tuple(sizes[:rank.value])
+    if out is None:
+        if blocked_output:
+            out = torch.empty(shape, dtype=torch.float16, device=a.device)
+        else:
+            n = shape[2]
+            out = torch.empty((shape[0], shape[1], (n + 15) // 16 * 16), dtype=torch.float16,
+                              device=a.device)[:, :, :n]
+    _call("thin_layout_bmm", _ref(desc(a)), _ref(desc(b)), ctypes.byref(L), _ref(desc(out)), _stream(stream))
+    return out
+
+
+def bmm(a, b, out=None, stream=None):
+    """Rank-3 a @ b (fp16, any strides), fp32 sums in reduction order."""
+    return layout_bmm(a, b, out=out, stream=stream)
+
+
+def channel_select(x, groups: int, begin: int, count: int, out=None, stream=None):
+    """Channels [begin, begin+count) of each of `groups` equal channel groups of
+    an N=1 blocked [1, C1, T, 16] fp16 tensor, packed back to back."""
+    sizes = (ctypes.c_int64 * 4)()
+    _call("thin_channel_select_shape", _ref(desc(x)), groups, begin, count, sizes)
+    out = torch.empty(tuple(sizes), dtype=torch.float16, device=x.device) if out is None else out
+    _call("thin_channel_select", _ref(desc(x)), groups, begin, count, _ref(desc(out)), _stream(stream))
     return out

@@ -1,23 +1,64 @@
-// libbmm_flow.so: the attention-bmm schemas of the reference library and its
-// aten::bmm kernel for the device (bmm_flow.cpp:342-359), registered so that
-// callers loading every flow library keep working; each raises -- the
-// contraction is not part of this backend (the attention row-softmax that
-// follows it is).
-#include <ATen/ATen.h>
+// libbmm_flow.so: thin_native_flow::bmm / layout_bmm / channel_select and the
+// device's aten::bmm (bmm_flow.cpp:253-359 of the reference) over the
+// thin_layout_bmm and thin_channel_select C entry points.  Unblocked results
+// are the [.., :n] view of a [batch, m, round_up(n, 16)] buffer, as the
+// reference returns them (bmm_flow.cpp:314,340).
+#include "thin_runtime.h"
+
 #include <torch/library.h>
 
-namespace {
-[[noreturn]] void unsupported(const char* name) {
-  TORCH_CHECK(false, "thin_native_flow.", name, " is not provided by the MI355X tensor-library backend");
+namespace bmm_flow {
+using namespace thin_rt;
+
+at::Tensor layout_bmm(const at::Tensor& a, const at::Tensor& b, bool transpose_a, bool transpose_b,
+                      bool blocked_output, int64_t groups, int64_t a_offset, int64_t a_channels, int64_t b_offset,
+                      int64_t b_channels) {
+  TORCH_CHECK(a.device().type() == kDevice && b.device() == a.device() && a.scalar_type() == at::kHalf &&
+                  b.scalar_type() == at::kHalf && (a.dim() == 3 || a.dim() == 4) && (b.dim() == 3 || b.dim() == 4) &&
+                  !a.requires_grad() && !b.requires_grad(),
+              "bmm requires inference-only same-device FP16 rank-3 or channel-blocked rank-4 tensors");
+  select(a.device());
+  thin_bmm_layout L{transpose_a, transpose_b, blocked_output, 0, groups, a_offset, a_channels, b_offset, b_channels};
+  thin_desc ad = desc(a), bd = desc(b);
+  int32_t rank = 0;
+  int64_t sizes[4] = {0, 0, 0, 0};
+  check(thin_layout_bmm_shape(&ad, &bd, &L, &rank, sizes), "thin_native_flow.layout_bmm");
+  at::Tensor result;
+  if (blocked_output) {
+    result = at::empty({sizes[0], sizes[1], sizes[2], sizes[3]}, a.options());
+  } else {
+    const int64_t pitch = (sizes[2] + 15) / 16 * 16;
+    result = at::empty({sizes[0], sizes[1], pitch}, a.options());
+    if (pitch != sizes[2]) result = result.slice(2, 0, sizes[2]);
+  }
+  thin_desc od = desc(result);
+  check(thin_layout_bmm(&ad, &bd, &L, &od, stream()), "thin_native_flow.layout_bmm");
+  after_launch();
+  return result;
 }
-at::Tensor bmm(const at::Tensor&, const at::Tensor&) { unsupported("bmm"); }
-at::Tensor aten_bmm(const at::Tensor&, const at::Tensor&) {
-  TORCH_CHECK(false, "thin aten bmm is not provided by the MI355X tensor-library backend");
+
+at::Tensor bmm(const at::Tensor& a, const at::Tensor& b) {
+  TORCH_CHECK(a.dim() == 3 && b.dim() == 3, "bmm requires rank-3 operands");
+  return layout_bmm(a, b, false, false, false, 0, 0, -1, 0, -1);
 }
-at::Tensor layout_bmm(const at::Tensor&, const at::Tensor&, bool, bool, bool, int64_t, int64_t, int64_t, int64_t,
-                      int64_t) { unsupported("layout_bmm"); }
-at::Tensor channel_select(const at::Tensor&, int64_t, int64_t, int64_t) { unsupported("channel_select"); }
-}  // namespace
+
+at::Tensor channel_select(const at::Tensor& x, int64_t groups, int64_t begin, int64_t count) {
+  TORCH_CHECK(x.device().type() == kDevice && x.scalar_type() == at::kHalf && x.dim() == 4 && x.size(0) == 1 &&
+                  x.size(3) == 16 && !x.requires_grad(),
+              "channel_select expects aligned N=1 FP16 blocked input");
+  select(x.device());
+  thin_desc xd = desc(x);
+  int64_t sizes[4] = {0, 0, 0, 0};
+  check(thin_channel_select_shape(&xd, groups, begin, count, sizes), "thin_native_flow.channel_select");
+  auto out = at::empty({sizes[0], sizes[1], sizes[2], sizes[3]}, x.options());
+  if (!out.numel()) return out;
+  thin_desc od = desc(out);
+  check(thin_channel_select(&xd, groups, begin, count, &od, stream()), "thin_native_flow.channel_select");
+  after_launch();
+  return out;
+}
+
+}  // namespace bmm_flow
 
 TORCH_LIBRARY_FRAGMENT(thin_native_flow, m) {
   m.def("bmm(Tensor a, Tensor b) -> Tensor");
@@ -26,9 +67,9 @@ TORCH_LIBRARY_FRAGMENT(thin_native_flow, m) {
   m.def("channel_select(Tensor x, int groups, int begin, int count) -> Tensor");
 }
 TORCH_LIBRARY_IMPL(thin_native_flow, PrivateUse1, m) {
-  m.impl("bmm", TORCH_FN(bmm));
-  m.impl("layout_bmm", TORCH_FN(layout_bmm));
-  m.impl("channel_select", TORCH_FN(channel_select));
+  m.impl("bmm", TORCH_FN(bmm_flow::bmm));
+  m.impl("layout_bmm", TORCH_FN(bmm_flow::layout_bmm));
+  m.impl("channel_select", TORCH_FN(bmm_flow::channel_select));
 }
 TORCH_LIBRARY_IMPL(thin_native_flow, AutogradPrivateUse1, m) {
   m.impl("bmm", torch::CppFunction::makeFallthrough());
@@ -36,5 +77,5 @@ TORCH_LIBRARY_IMPL(thin_native_flow, AutogradPrivateUse1, m) {
   m.impl("channel_select", torch::CppFunction::makeFallthrough());
 }
 TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
-  m.impl("bmm", TORCH_FN(aten_bmm));
+  m.impl("bmm", TORCH_FN(bmm_flow::bmm));
 }

@@ -21,7 +21,7 @@ LIBS = {
     "libconv_flow.so": ["conv_flow.cpp"],
     "libselection_flow.so": ["selection.cpp"],
     "libthin_blocked.so": ["blocked.cpp"],
-    "libbmm_flow.so": ["bmm_flow_stub.cpp"],
+    "libbmm_flow.so": ["bmm_flow.cpp"],
     "libdepthwise_flow.so": ["depthwise_flow_stub.cpp"],
 }
 
