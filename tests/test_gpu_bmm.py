@@ -201,3 +201,30 @@ def test_bmm_errors(gpu):
             fn()
     with pytest.raises(capi.ThinError, match="out must be"):
         capi.bmm(h(2, 3, 4), h(2, 4, 6), out=h(2, 3, 5))
+
+
+@pytest.mark.parametrize("key", [80, 128, 528])
+def test_streamed_long_reductions(gpu, key):
+    """q^T k with K = key channels: the streamed-column kernel's 64-step
+    staging rounds (K > 64), several vector rounds, a partial last round, and
+    (K = 528) two rounds of staged rows."""
+    from thintnpu_amd import capi
+    heads, tokens = 2, 70
+    source = torch.randn(heads, 2 * key // 16, tokens, 16, generator=gen(key)).half()
+    q, k = source.to(gpu).split((key // 16, key // 16), 1)
+    qr, kr = source.split((key // 16, key // 16), 1)
+    assert bits_equal(capi.layout_bmm(q, k, True, False, False), ob.layout_bmm(qr, kr, True, False, False))
+
+
+@pytest.mark.parametrize("k", [21, 77])
+def test_streamed_reduction_tail(gpu, k):
+    """Columns contiguous along k at a 24-element stride with K % 8 != 0: the
+    streamed kernel's whole vectors plus its scalar tail."""
+    from thintnpu_amd import capi
+    batch, m, n = 2, 9, 70
+    pitch = (k + 7) // 8 * 8 + 8
+    a = torch.randn(batch, m, k, generator=gen(k)).half()
+    store = torch.randn(batch, n, pitch, generator=gen(k + 1)).half()
+    b = store[:, :, :k].transpose(1, 2)          # [batch, k, n], column stride `pitch`
+    bd = store.to(gpu)[:, :, :k].transpose(1, 2)
+    assert bits_equal(capi.bmm(a.to(gpu), bd), ob.sequential_bmm(a, b))
