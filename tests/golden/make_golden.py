@@ -23,6 +23,7 @@ import torch
 ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 
+from oracle import bmm as ob  # noqa: E402
 from oracle import elementwise as ew  # noqa: E402
 from oracle import movement as mv  # noqa: E402
 from oracle import reductions as rd  # noqa: E402
@@ -123,6 +124,18 @@ def build() -> dict[str, np.ndarray]:
         ref = sel.select(sx, 20, agnostic)
         for name in sel.TRACE_NAMES:
             g[f"sel_{int(agnostic)}_{name}"] = store(ref[name])
+    # attention contractions: grouped q^T k, v p^T with the blocked output and
+    # channel select over one [1,6,20,16] QKV tensor (2 heads of 16+16+16
+    # channels), and a plain bmm whose large sums overflow to inf
+    qkv = (torch.randn(1, 6, 20, 16, generator=gen(894)) * 2).half()
+    prob = torch.rand(2, 20, 20, generator=gen(895)).half()
+    g["bmm_qkv"], g["bmm_p"] = store(qkv), store(prob)
+    g["bmm_qk"] = store(ob.layout_bmm(qkv, qkv, True, False, False, 2, 0, 16, 16, 16))
+    g["bmm_vp"] = store(ob.layout_bmm(qkv, prob, False, True, True, 2, 32, 16))
+    g["bmm_sel"] = store(ob.channel_select(qkv, 2, 32, 16))
+    ma = (torch.randn(3, 7, 40, generator=gen(896)) * 100).half()
+    mb = (torch.randn(3, 40, 9, generator=gen(897)) * 100).half()
+    g["bmm_a"], g["bmm_b"], g["bmm_ab"] = store(ma), store(mb), store(ob.bmm(ma, mb))
     return g
 
 

@@ -1,6 +1,7 @@
 """The oracle against the committed golden vectors (tests/golden/golden.npz).
 
-Closed-form ops (add/sub/mul/div with alpha), data movement and selection must
+Closed-form ops (add/sub/mul/div with alpha, the sequential-sum bmm), data
+movement and selection must
 reproduce the stored bits on any torch build.  Exp-based ops (sigmoid, SiLU,
 fused chains, softmax, DFL) are bit-identical on the torch version and CPU ISA
 the manifest records and within one fp16 ulp (fp32: 1e-6 relative) elsewhere,
@@ -8,6 +9,7 @@ since torch's vectorised exp may move an ulp across versions and ISAs."""
 import pytest
 import torch
 
+from oracle import bmm as ob
 from oracle import elementwise as ew
 from oracle import movement as mv
 from oracle import reductions as rd
@@ -77,3 +79,12 @@ def test_selection_bits(agnostic):
     ref = sel.select(G["sel_x"], 20, agnostic)
     for name in sel.TRACE_NAMES:
         assert bits_equal(ref[name], G[f"sel_{int(agnostic)}_{name}"]), name
+
+
+def test_bmm_bits():
+    qkv, p = G["bmm_qkv"], G["bmm_p"]
+    assert bits_equal(ob.layout_bmm(qkv, qkv, True, False, False, 2, 0, 16, 16, 16), G["bmm_qk"])
+    assert bits_equal(ob.layout_bmm(qkv, p, False, True, True, 2, 32, 16), G["bmm_vp"])
+    assert bits_equal(ob.channel_select(qkv, 2, 32, 16), G["bmm_sel"])
+    assert bits_equal(ob.bmm(G["bmm_a"], G["bmm_b"]), G["bmm_ab"])
+    assert G["bmm_ab"].isinf().any() and not G["bmm_ab"].isnan().any()

@@ -70,3 +70,13 @@ def test_selection(gpu, golden, agnostic):
         want = G[f"sel_{int(agnostic)}_{theirs}"]
         assert got.shape == want.shape, (mine, got.shape, want.shape)
         assert bits_equal(got, want.to(got.dtype)), mine
+
+
+def test_bmm(gpu, golden):
+    from thintnpu_amd import capi
+    G = golden
+    qkv, p = G["bmm_qkv"].to(gpu), G["bmm_p"].to(gpu)
+    assert bits_equal(capi.layout_bmm(qkv, qkv, True, False, False, 2, 0, 16, 16, 16).cpu(), G["bmm_qk"])
+    assert bits_equal(capi.layout_bmm(qkv, p, False, True, True, 2, 32, 16).cpu(), G["bmm_vp"])
+    assert bits_equal(capi.channel_select(qkv, 2, 32, 16).cpu(), G["bmm_sel"])
+    assert bits_equal(capi.bmm(G["bmm_a"].to(gpu), G["bmm_b"].to(gpu)).cpu(), G["bmm_ab"])
