@@ -2,6 +2,7 @@
 
 Everything is built in-tree:
   thintnpu_amd/libthin_hip.so        C-ABI kernel library (include/thin_hip.h), hipcc
+  thintnpu_amd/capi_selftest         plain C consumer of the C ABI (no PyTorch), gcc
   thin_backend/lib*.so               PrivateUse1 registrations (libtorch + HIP runtime), g++
 
 Run ``python -m thintnpu_amd.build`` (or ``__graft_entry__.build()``).  Every
@@ -79,8 +80,26 @@ def build_hip(verbose: bool = False) -> Path:
     return HIP_LIB
 
 
+SELFTEST = PKG / "capi_selftest"
+
+
+def build_selftest(verbose: bool = False) -> Path:
+    """A plain C program over include/thin_hip.h (no PyTorch): hipMalloc'd
+    buffers, its own stream, exact checks on the host."""
+    cc = os.environ.get("CC", "gcc")
+    cmd = [cc, "-std=c11", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", f"-I{INCLUDE}",
+           str(PKG / "csrc" / "capi_selftest.c"), "-o", str(SELFTEST) + ".tmp", f"-L{HIP_LIB.parent}", "-lthin_hip",
+           f"-L{ROCM / 'lib'}", "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}"]
+    if verbose:
+        print(" ".join(cmd), file=sys.stderr)
+    _run(cmd)
+    os.replace(str(SELFTEST) + ".tmp", SELFTEST)
+    return SELFTEST
+
+
 def build(verbose: bool = False) -> None:
     build_hip(verbose)
+    build_selftest(verbose)
     try:
         from thintnpu_amd import torch_build  # noqa: F401  (glue recipe, optional until present)
     except ImportError:
