@@ -275,6 +275,19 @@ def op_decode(capi, dev, n, rotate=True):
     return (lambda st: capi.detect_decode(st[0], st[1], shapes, strides, out=st[2])), sets, algo
 
 
+def op_decode_direct(capi, dev, n, rotate=True):
+    """YOLO26 head decode (reg_max = 1, distances as given): [n,4,8400] +
+    sigmoid [n,80,8400] -> [n,84,8400]."""
+    a = 8400
+    algo = n * a * 2 * (4 + 80 + 84)
+    g = torch.Generator(device=dev).manual_seed(8)
+    sets = rotated(lambda i: ((torch.rand((n, 4, a), generator=g, device=dev) * 20).half(),
+                              (torch.randn((n, 80, a), generator=g, device=dev) * 2 - 4).half(),
+                              torch.empty((n, 84, a), dtype=torch.float16, device=dev)), algo, rotate)
+    shapes, strides = [(80, 80), (40, 40), (20, 20)], [8.0, 16.0, 32.0]
+    return (lambda st: capi.detect_decode(st[0], st[1], shapes, strides, out=st[2])), sets, algo
+
+
 def op_permute(capi, dev, n, rotate=True):
     """Materialize NCHW [n,64,80,80] as NHWC: x.permute(0,2,3,1).contiguous()."""
     algo = n * 64 * 80 * 80 * 2 * 2
@@ -366,6 +379,7 @@ def op_rows(capi, dev):
         rows.append(("maxpool_k5_256x20x20", "SPPF", n, lambda r, n=n: op_maxpool(capi, dev, n, r)))
         rows.append(("sppf_k5x3_cat_256x20x20", "SPPF", n, lambda r, n=n: op_sppf(capi, dev, n, r)))
         rows.append(("detect_decode_64+80x8400", "C4", n, lambda r, n=n: op_decode(capi, dev, n, r)))
+        rows.append(("detect_decode_4+80x8400", "C5", n, lambda r, n=n: op_decode_direct(capi, dev, n, r)))
         rows.append(("permute_nchw_to_nhwc_64x80x80", "MAT", n, lambda r, n=n: op_permute(capi, dev, n, r)))
     rows.append(("attn_qk_4x32x400", "ATTN", 1, lambda r: op_attn_qk(capi, dev, 1, r)))
     rows.append(("attn_pv_4x64x400", "ATTN", 1, lambda r: op_attn_pv(capi, dev, 1, r)))
@@ -438,6 +452,11 @@ def cpu_op(name, n):
         b, sc = h16(n, 64, 8400) * 3, h16(n, 80, 8400)
         shapes, strides = [(80, 80), (40, 40), (20, 20)], [8.0, 16.0, 32.0]
         return (lambda: dt.detect_decode(b, sc, shapes, strides)), n * 8400 * 2 * (64 + 80 + 84)
+    if name == "detect_decode_4+80x8400":
+        from oracle import detect as dt  # the CPU decode sequence, timed
+        b, sc = (torch.rand(n, 4, 8400, generator=g) * 20).half(), h16(n, 80, 8400)
+        shapes, strides = [(80, 80), (40, 40), (20, 20)], [8.0, 16.0, 32.0]
+        return (lambda: dt.detect_decode(b, sc, shapes, strides)), n * 8400 * 2 * (4 + 80 + 84)
     if name == "permute_nchw_to_nhwc_64x80x80":
         x = h16(n, 64, 80, 80)
         return (lambda: x.permute(0, 2, 3, 1).contiguous()), x.numel() * 4

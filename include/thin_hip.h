@@ -230,7 +230,9 @@ typedef struct thin_select_trace {
 } thin_select_trace;
 
 /* Anchor-free detect-head decode in one launch: the DFL expectation of
- * boxes [B,64,A] (bit-identical to thin_dfl_expect with fp16 output), the
+ * boxes [B,64,A] (bit-identical to thin_dfl_expect with fp16 output), or
+ * boxes [B,4,A] taken as the distances themselves (reg_max = 1 heads such as
+ * YOLO26's, whose module.dfl is the identity), the
  * distances applied to the per-level grid cell centres (x + 0.5, y + 0.5) as
  * lower = centre - d[0:2], upper = centre + d[2:4], scaled by the level stride
  * as xyxy (lower, upper) or xywh ((lower+upper)/2, upper-lower), each step one

@@ -11,7 +11,10 @@ Restates anchorfree_predictions (whole_blocked.py:118-146; YOLO26.md:30-38):
                             step an fp16 tensor op (whole_blocked.py:136-143)
   detect_decode(...)     -- cat(box_decode(dfl_expect(boxes)), sigmoid(scores))
                             with the fused DFL expectation (fp16 output) of
-                            oracle.reductions (whole_blocked.py:144)
+                            oracle.reductions (whole_blocked.py:135,144); for
+                            [B,4,A] boxes (reg_max = 1, e.g. YOLO26, whose
+                            module.dfl is the identity) the boxes are the
+                            distances (YOLO26.md:30-38)
 
 Pinning (tests/test_oracle_detect.py): the grid against a brute-force loop;
 each fp16 box step against float64 arithmetic rounded once (fp16 tensor ops
@@ -46,5 +49,5 @@ def box_decode(distance: torch.Tensor, shapes, strides, xywh: bool = False) -> t
 
 
 def detect_decode(boxes: torch.Tensor, scores: torch.Tensor, shapes, strides, xywh: bool = False) -> torch.Tensor:
-    distance = rd.dfl_expect(boxes, torch.float16)
+    distance = boxes if boxes.shape[1] == 4 else rd.dfl_expect(boxes, torch.float16)
     return torch.cat((box_decode(distance, shapes, strides, xywh), ew.sigmoid(scores)), 1)

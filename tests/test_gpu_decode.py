@@ -111,3 +111,39 @@ def test_offsets_beyond_4gib(gpu):
     finally:
         del far, storage
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("xywh", [False, True])
+def test_decode_direct_distances(gpu, xywh):
+    """reg_max = 1 heads (YOLO26, whose module.dfl is the identity:
+    whole_blocked.py:135; YOLO26.md:30-38): boxes [B,4,A] are the distances.
+    Boxes bit-exact against the oracle's fp16 steps, scores within 2 ulp; the
+    two-anchor and the single-anchor (unaligned view) forms."""
+    from thintnpu_amd import capi
+    from tests.helpers import gen
+    shapes, strides = YOLO
+    a = 8400
+    dist = (torch.rand(2, 4, a, generator=gen(31)) * 20).half()
+    dist[0, 1, 5] = float("nan")
+    dist[1, 2, 9] = float("inf")
+    scores = normal16((2, 80, a), 32, mean=-4.0, std=2.0)
+    got = capi.detect_decode(dist.to(gpu), scores.to(gpu), shapes, strides, xywh).cpu()
+    ref = dt.detect_decode(dist, scores, shapes, strides, xywh)
+    nan = torch.isnan(ref[:, :4])
+    assert torch.equal(torch.isnan(got[:, :4]), nan)
+    assert bits_equal(got[:, :4][~nan], ref[:, :4][~nan])
+    assert_ulp(got[:, 4:], ref[:, 4:], 2, "scores")
+    # distances read through an unaligned strided view (single-anchor path)
+    parent = torch.zeros((2, 6, a + 1), dtype=torch.float16)
+    parent[:, 1:5, 1:] = dist
+    view = parent.to(gpu)[:, 1:5, 1:]
+    got = capi.detect_decode(view, scores.to(gpu), shapes, strides, xywh).cpu()
+    assert torch.equal(torch.isnan(got[:, :4]), nan)
+    assert bits_equal(got[:, :4][~nan], ref[:, :4][~nan])
+    # the dispatcher op takes the same [B,4,A] boxes
+    import thin_backend
+    thin_backend.load_flow_libraries()
+    with torch.inference_mode():
+        flat = [v for hw in shapes for v in hw]
+        npu = torch.ops.thin_fused.detect_decode(dist.to("npu"), scores.to("npu"), flat, strides, xywh).cpu()
+    assert bits_equal(npu, capi.detect_decode(dist.to(gpu), scores.to(gpu), shapes, strides, xywh).cpu())

@@ -59,3 +59,16 @@ def test_closed_forms(xywh):
     d = hot.view(1, 4, 1).half().expand(1, 4, a)
     assert bits_equal(out[:, :4], dt.box_decode(d, SHAPES, STRIDES, xywh))
     assert (out[:, 4:] == 0.5).all()
+
+
+def test_direct_distances_closed_form():
+    """[B,4,A] boxes (reg_max = 1) are the distances: with small integer
+    distances every fp16 step is exact, so xyxy equals float64 arithmetic."""
+    a = sum(h * w for h, w in SHAPES)
+    anchors, scale = dt.grid(SHAPES, STRIDES)
+    d = torch.tensor([1.0, 2.0, 3.0, 4.0]).view(1, 4, 1).expand(1, 4, a).half()
+    out = dt.detect_decode(d, torch.zeros(1, 2, a, dtype=torch.float16), SHAPES, STRIDES)
+    cx, cy, s = anchors[0].double(), anchors[1].double(), scale[0].double()
+    want = torch.stack(((cx - 1) * s, (cy - 2) * s, (cx + 3) * s, (cy + 4) * s))[None]
+    assert torch.equal(out[:, :4].double(), want)
+    assert (out[:, 4:] == 0.5).all()

@@ -306,8 +306,9 @@ def dfl_expect(x, out_dtype=None, out=None, stream=None):
 
 
 def detect_decode(boxes, scores, shapes, strides, xywh: bool = False, out=None, stream=None):
-    """Anchor-free head decode: [B,64,A] box logits + [B,nc,A] class logits ->
-    [B,4+nc,A] fp16 (boxes by DFL + grid + stride, scores by sigmoid).
+    """Anchor-free head decode: [B,64,A] box logits (or [B,4,A] distances of a
+    reg_max = 1 head) + [B,nc,A] class logits -> [B,4+nc,A] fp16 (boxes by DFL
+    (or as given) + grid + stride, scores by sigmoid).
     shapes: per-level (h, w); strides: per-level stride."""
     b, _, a = boxes.shape
     nc = scores.shape[1]

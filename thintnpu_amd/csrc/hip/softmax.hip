@@ -336,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
 constexpr int kMaxLevels = 8;
 
 struct DecodePlan {
-  const _Float16* boxes;  // [B,64,A]
+  const _Float16* boxes;  // [B,64,A] DFL logits, or [B,4,A] distances (direct)
   const _Float16* scores; // [B,nc,A]
   _Float16* out;          // [B,4+nc,A]
   int64_t bb, bc, ba, sb, sc, sa, ob, oc, oa;  // element strides
@@ -352,6 +352,7 @@ struct DecodePlan {
   uint32_t score_units;   // B * nc * svecs
   FastDiv div_apairs, div_svecs, div_nc;
   int32_t xywh;
+  int32_t direct;         // boxes are the distances themselves (reg_max = 1 heads)
   uint32_t boxes_bytes;   // byte extent of boxes from its base (buffer-load forms)
 };
 
@@ -370,7 +371,22 @@ __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
     const uint32_t b = ba_ >> 1, axis = ba_ & 1u;
     _Float16 bins[16][VB];
     float lo[VB], hi[VB];
-    if constexpr (LOAD > 0) {
+    if (p.direct) {
+      // distances as they are: the lt / rb channels of this axis
+      const _Float16* xc = p.boxes + b * p.bb + (int64_t)a0 * p.ba;
+      if constexpr (VB == 2) {  // anchor pairs are 4-byte aligned here (host checks)
+        typedef _Float16 hv __attribute__((ext_vector_type(2)));
+        const hv l = *reinterpret_cast<const hv*>(xc + (int64_t)axis * p.bc);
+        const hv h = *reinterpret_cast<const hv*>(xc + (int64_t)(axis + 2) * p.bc);
+        lo[0] = (float)l[0];
+        lo[1] = (float)l[1];
+        hi[0] = (float)h[0];
+        hi[1] = (float)h[1];
+      } else {
+        lo[0] = (float)xc[(int64_t)axis * p.bc];
+        hi[0] = (float)xc[(int64_t)(axis + 2) * p.bc];
+      }
+    } else if constexpr (LOAD > 0) {
       const __amdgpu_buffer_rsrc_t rs = dev::buffer_rsrc(p.boxes, p.boxes_bytes);
       const uint32_t bc = 2u * (uint32_t)p.bc;
       const uint32_t off = 2u * (b * (uint32_t)p.bb + a0 * (uint32_t)p.ba) + axis * 16u * bc;
@@ -656,11 +672,11 @@ extern "C" thin_status thin_detect_decode(const thin_desc* boxes, const thin_des
                "detect_decode: invalid descriptor");
   THIN_REQUIRE(boxes->dtype == THIN_F16 && scores->dtype == THIN_F16 && out->dtype == THIN_F16 &&
                boxes->rank == 3 && scores->rank == 3 && out->rank == 3, THIN_ERR_INVALID,
-               "detect_decode takes float16 boxes [B,64,A], scores [B,nc,A] and out [B,4+nc,A]");
+               "detect_decode takes float16 boxes [B,64,A] or [B,4,A], scores [B,nc,A] and out [B,4+nc,A]");
   const int64_t B = boxes->sizes[0], A = boxes->sizes[2], nc = scores->sizes[1];
-  THIN_REQUIRE(boxes->sizes[1] == 64 && scores->sizes[0] == B && scores->sizes[2] == A && out->sizes[0] == B &&
-               out->sizes[1] == 4 + nc && out->sizes[2] == A, THIN_ERR_INVALID,
-               "detect_decode expects boxes [B,64,A], scores [B,nc,A], out [B,4+nc,A]");
+  THIN_REQUIRE((boxes->sizes[1] == 64 || boxes->sizes[1] == 4) && scores->sizes[0] == B && scores->sizes[2] == A &&
+               out->sizes[0] == B && out->sizes[1] == 4 + nc && out->sizes[2] == A, THIN_ERR_INVALID,
+               "detect_decode expects boxes [B,64,A] or [B,4,A], scores [B,nc,A], out [B,4+nc,A]");
   THIN_REQUIRE(levels >= 1 && levels <= kMaxLevels && level_hw && level_stride, THIN_ERR_INVALID,
                "detect_decode takes 1..%d levels", kMaxLevels);
   DecodePlan p;
@@ -688,6 +704,7 @@ extern "C" thin_status thin_detect_decode(const thin_desc* boxes, const thin_des
   p.ob = out->strides[0]; p.oc = out->strides[1]; p.oa = out->strides[2];
   p.nc = (uint32_t)nc;
   p.xywh = xywh ? 1 : 0;
+  p.direct = boxes->sizes[1] == 4 ? 1 : 0;
   const bool vb = A % 2 == 0 && p.ba == 1 && p.oa == 1 && aligned(boxes->data, 4) && aligned(out->data, 4) &&
                   p.bb % 2 == 0 && p.bc % 2 == 0 && p.ob % 2 == 0 && p.oc % 2 == 0;
   const bool vs = A % 8 == 0 && p.sa == 1 && p.oa == 1 && aligned(scores->data, 16) && aligned(out->data, 16) &&

@@ -394,13 +394,14 @@ at::Tensor dfl_expect(const at::Tensor& x, bool fp32_output) {
 }
 
 // Anchor-free head decode (whole_blocked.py:118-146): shapes = flattened
-// per-level (h, w), strides = per-level strides.
+// per-level (h, w), strides = per-level strides; boxes are DFL logits
+// [B,64,A] or, for reg_max = 1 heads, the distances [B,4,A].
 void decode_check(const at::Tensor& boxes, const at::Tensor& scores, at::IntArrayRef shapes,
                   at::ArrayRef<double> strides) {
   TORCH_CHECK(boxes.scalar_type() == at::kHalf && scores.scalar_type() == at::kHalf && boxes.dim() == 3 &&
-                  scores.dim() == 3 && boxes.size(1) == 64 && scores.size(0) == boxes.size(0) &&
-                  scores.size(2) == boxes.size(2),
-              "detect_decode expects float16 boxes [B,64,A] and scores [B,nc,A]");
+                  scores.dim() == 3 && (boxes.size(1) == 64 || boxes.size(1) == 4) &&
+                  scores.size(0) == boxes.size(0) && scores.size(2) == boxes.size(2),
+              "detect_decode expects float16 boxes [B,64,A] (DFL logits) or [B,4,A] (distances) and scores [B,nc,A]");
   TORCH_CHECK(shapes.size() % 2 == 0 && shapes.size() / 2 == strides.size() && !strides.empty() &&
                   strides.size() <= 8,
               "detect_decode expects (h, w) per level and one stride per level (1..8 levels)");
