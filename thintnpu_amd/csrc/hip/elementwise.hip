@@ -421,11 +421,6 @@ template <bool NTL, bool NTS>
 __global__ __launch_bounds__(kThreads) void affine_silu_flat_kernel(AffineFlatPlan p) {
   constexpr int U = 2;
   __shared__ h8v sb[2][2 * kFlatMaxC1];
-  for (uint32_t i = threadIdx.x; i < 2 * p.c1; i += kThreads) {
-    sb[0][i] = p.s[(i >> 1) * p.s_c1 + (i & 1u)];
-    sb[1][i] = p.b[(i >> 1) * p.b_c1 + (i & 1u)];
-  }
-  __syncthreads();
   const uint32_t tile = blockIdx.x * (kThreads * U);
   h8v v[U];
   uint32_t oo[U], q[U];
@@ -441,6 +436,14 @@ __global__ __launch_bounds__(kThreads) void affine_silu_flat_kernel(AffineFlatPl
       v[u] = NTL ? __builtin_nontemporal_load(src) : *src;
     }
   }
+  // Scale/bias staging goes after the x loads are issued: its loads and the
+  // barrier then overlap the x round trip instead of preceding it (one round
+  // trip less per block; 6.35 -> 5.7 us for [32,512,20,20]).
+  for (uint32_t i = threadIdx.x; i < 2 * p.c1; i += kThreads) {
+    sb[0][i] = p.s[(i >> 1) * p.s_c1 + (i & 1u)];
+    sb[1][i] = p.b[(i >> 1) * p.b_c1 + (i & 1u)];
+  }
+  __syncthreads();
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const uint32_t i = tile + u * kThreads + threadIdx.x;
