@@ -109,8 +109,8 @@ def time_launches(launch, sets, iters, rounds=5):
 # copy map_dense_kernel<OpCopy> over the same [32,8,80,80,16] fp16 tensor
 # (104857600 B read + written), from `bench.py --profile dominant|copy --iters 20`
 # (profiles/affine_silu_flat_n32_128x80x80_pmc.md).
-PMC_KIB = {"dominant": {"FETCH_SIZE": 25619.0, "WRITE_SIZE": 51200.375},
-           "copy": {"FETCH_SIZE": 25610.0, "WRITE_SIZE": 51250.625}}
+PMC_KIB = {"dominant": {"FETCH_SIZE": 25621.0, "WRITE_SIZE": 51200.0},
+           "copy": {"FETCH_SIZE": 25606.5, "WRITE_SIZE": 51246.375}}
 COPY_BYTES_EACH_WAY = 52428800
 
 
@@ -652,7 +652,7 @@ def main():
     achieved = algo / dom_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": dominant_traffic(),
-                "kernel": "affine_silu_flat_kernel<true, true> (thin_affine_silu)",
+                "kernel": "affine_silu_flat_kernel<2, true, true> (thin_affine_silu)",
                 "launch": f"N=32 C,H,W={C2_SHAPES[0]}: {algo} algorithmic bytes, avg {dom_s * 1e6:.2f} us",
                 "traffic_note": "HBM bytes per launch = FETCH_SIZE x fetch factor + WRITE_SIZE x write factor, "
                                 "factors from a plain 16-byte copy of the same tensor (rocprofv3 --pmc, "

@@ -192,7 +192,7 @@ def test_affine_silu_c2(gpu, n, chw):
 
 
 @pytest.mark.parametrize("case", ["per_image_scale", "channel_stride", "wide_c1", "tiny_planes",
-                                  "narrowed_out", "strided_scale", "n1_offset"])
+                                  "narrowed_out", "strided_scale", "n1_offset", "mid_size_tail"])
 def test_affine_silu_layouts(gpu, case):
     """Every NC1HWC0 layout the fused kernel accepts, flat-span and per-plane
     forms alike, against the op-by-op fp16 chain; outputs written through a
@@ -200,7 +200,10 @@ def test_affine_silu_layouts(gpu, case):
     from thintnpu_amd import capi
     n, c, h, w = {"per_image_scale": (3, 64, 5, 7), "channel_stride": (2, 128, 6, 10),
                   "wide_c1": (2, 4096, 2, 3), "tiny_planes": (5, 16, 1, 1), "narrowed_out": (4, 96, 9, 11),
-                  "strided_scale": (2, 64, 8, 8), "n1_offset": (1, 256, 20, 20)}[case]
+                  "strided_scale": (2, 64, 8, 8), "n1_offset": (1, 256, 20, 20),
+                  # 209,824 vectors (3.4 MB): two vectors per thread with cached loads,
+                  # a partial last block
+                  "mid_size_tail": (2, 128, 79, 83)}[case]
     x, s, b = c2_inputs(n, c, h, w, seed=len(case))
     if case == "per_image_scale":
         s = (torch.rand((n, c // 16, 1, 1, 16), generator=gen(5)) + 0.5).half()

@@ -417,9 +417,8 @@ struct AffineFlatPlan {
   uint32_t c1;            // channel blocks per row
 };
 
-template <bool NTL, bool NTS>
+template <int U, bool NTL, bool NTS>
 __global__ __launch_bounds__(kThreads) void affine_silu_flat_kernel(AffineFlatPlan p) {
-  constexpr int U = 2;
   __shared__ h8v sb[2][2 * kFlatMaxC1];
   const uint32_t tile = blockIdx.x * (kThreads * U);
   h8v v[U];
@@ -485,10 +484,17 @@ bool try_affine_flat(const thin_desc* x, const thin_desc* sc, const thin_desc* b
   p.s_c1 = (uint32_t)(sc->strides[1] / 8);
   p.b_c1 = (uint32_t)(b->strides[1] / 8);
   p.c1 = (uint32_t)c1;
-  const uint32_t grid = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
+  // Two vectors per thread, or one when that leaves fewer than 256 blocks
+  // (a single small image): then more blocks shorten the launch.
+  const uint32_t grid2 = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
   const bool nt = total * 16 >= kStreamingBytes;
-  if (nt) hipLaunchKernelGGL((affine_silu_flat_kernel<true, true>), dim3(grid), dim3(kThreads), 0, stream, p);
-  else hipLaunchKernelGGL((affine_silu_flat_kernel<false, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+  if (nt)
+    hipLaunchKernelGGL((affine_silu_flat_kernel<2, true, true>), dim3(grid2), dim3(kThreads), 0, stream, p);
+  else if (grid2 >= 256)
+    hipLaunchKernelGGL((affine_silu_flat_kernel<2, false, false>), dim3(grid2), dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((affine_silu_flat_kernel<1, false, false>), dim3((uint32_t)((total + kThreads - 1) / kThreads)),
+                       dim3(kThreads), 0, stream, p);
   return true;
 }
 
