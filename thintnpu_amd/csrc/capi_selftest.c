@@ -199,6 +199,86 @@ int main(void) {
     HIP(hipFree(dout));
   }
 
+  /* 5. pack NCHW [1,20,3,5] -> NC1HWC0 [1,2,3,5,16] (channels 20..31 zero),
+   *    then unpack back to NCHW: both bit copies */
+  {
+    enum { C = 20, H = 3, W = 5, C1 = 2 };
+    uint16_t hx[C * H * W], hb[C1 * H * W * 16], hu[C * H * W];
+    for (int i = 0; i < C * H * W; ++i) hx[i] = (uint16_t)(0x3c00 + i);
+    uint16_t *dx, *db, *du;
+    HIP(hipMalloc((void**)&dx, sizeof hx));
+    HIP(hipMalloc((void**)&db, sizeof hb));
+    HIP(hipMalloc((void**)&du, sizeof hu));
+    HIP(hipMemcpy(dx, hx, sizeof hx, hipMemcpyHostToDevice));
+    const int64_t sx[4] = {1, C, H, W}, sb[5] = {1, C1, H, W, 16};
+    thin_desc x = desc(dx, THIN_F16, 4, sx), b = desc(db, THIN_F16, 5, sb), u = desc(du, THIN_F16, 4, sx);
+    CHECK(thin_pack_nc1hwc0(&x, &b, s) == THIN_OK, "thin_pack_nc1hwc0: %s", thin_last_error());
+    CHECK(thin_unpack_nc1hwc0(&b, &u, s) == THIN_OK, "thin_unpack_nc1hwc0: %s", thin_last_error());
+    HIP(hipStreamSynchronize(s));
+    HIP(hipMemcpy(hb, db, sizeof hb, hipMemcpyDeviceToHost));
+    HIP(hipMemcpy(hu, du, sizeof hu, hipMemcpyDeviceToHost));
+    int bad = 0;
+    for (int c = 0; c < C1 * 16; ++c)
+      for (int p = 0; p < H * W; ++p) {
+        const uint16_t want = c < C ? hx[c * H * W + p] : 0;
+        bad += hb[((c / 16) * H * W + p) * 16 + c % 16] != want;
+      }
+    CHECK(bad == 0, "pack: %d wrong", bad);
+    CHECK(memcmp(hu, hx, sizeof hx) == 0, "unpack did not restore the NCHW input");
+    HIP(hipFree(dx));
+    HIP(hipFree(db));
+    HIP(hipFree(du));
+  }
+
+  /* 6. nearest 2x upsample [1,1,2,3,16] -> [1,1,4,6,16] and a k3 max pool of
+   *    the result (distinct small integers: every maximum exact), then fill */
+  {
+    enum { H = 2, W = 3 };
+    uint16_t hx[H * W * 16], hy[4 * H * W * 16], hp[4 * H * W * 16];
+    for (int i = 0; i < H * W * 16; ++i) hx[i] = half_of_int((i * 37) % 101 - 50);
+    uint16_t *dx, *dy, *dp;
+    HIP(hipMalloc((void**)&dx, sizeof hx));
+    HIP(hipMalloc((void**)&dy, sizeof hy));
+    HIP(hipMalloc((void**)&dp, sizeof hp));
+    HIP(hipMemcpy(dx, hx, sizeof hx, hipMemcpyHostToDevice));
+    const int64_t sx[5] = {1, 1, H, W, 16}, sy[5] = {1, 1, 2 * H, 2 * W, 16};
+    thin_desc x = desc(dx, THIN_F16, 5, sx), y = desc(dy, THIN_F16, 5, sy), p = desc(dp, THIN_F16, 5, sy);
+    CHECK(thin_upsample2x_nc1hwc0(&x, &y, s) == THIN_OK, "thin_upsample2x_nc1hwc0: %s", thin_last_error());
+    CHECK(thin_maxpool_nc1hwc0(&y, 3, &p, s) == THIN_OK, "thin_maxpool_nc1hwc0: %s", thin_last_error());
+    HIP(hipStreamSynchronize(s));
+    HIP(hipMemcpy(hy, dy, sizeof hy, hipMemcpyDeviceToHost));
+    HIP(hipMemcpy(hp, dp, sizeof hp, hipMemcpyDeviceToHost));
+    int bad_up = 0, bad_pool = 0;
+    for (int r = 0; r < 2 * H; ++r)
+      for (int c = 0; c < 2 * W; ++c)
+        for (int l = 0; l < 16; ++l) {
+          bad_up += hy[(r * 2 * W + c) * 16 + l] != hx[((r / 2) * W + c / 2) * 16 + l];
+          int best = -100000;
+          for (int dr = -1; dr <= 1; ++dr)
+            for (int dc = -1; dc <= 1; ++dc) {
+              const int rr = r + dr, cc = c + dc;
+              if (rr < 0 || rr >= 2 * H || cc < 0 || cc >= 2 * W) continue; /* taps outside the plane skipped */
+              const int v = int_of_half(hx[((rr / 2) * W + cc / 2) * 16 + l]);
+              if (v > best) best = v;
+            }
+          bad_pool += int_of_half(hp[(r * 2 * W + c) * 16 + l]) != best;
+        }
+    CHECK(bad_up == 0, "upsample2x: %d wrong", bad_up);
+    CHECK(bad_pool == 0, "maxpool k3: %d wrong", bad_pool);
+    /* fill the pooled tensor with 3.0 (fp16 0x4200) */
+    CHECK(thin_fill(&p, 3.0, 0, s) == THIN_OK, "thin_fill: %s", thin_last_error());
+    HIP(hipStreamSynchronize(s));
+    HIP(hipMemcpy(hp, dp, sizeof hp, hipMemcpyDeviceToHost));
+    int bad_fill = 0;
+    for (int i = 0; i < 4 * H * W * 16; ++i) bad_fill += hp[i] != 0x4200u;
+    CHECK(bad_fill == 0, "fill: %d wrong", bad_fill);
+    /* an even pool kernel is rejected */
+    CHECK(thin_maxpool_nc1hwc0(&y, 4, &p, s) == THIN_ERR_INVALID, "maxpool k4 not rejected");
+    HIP(hipFree(dx));
+    HIP(hipFree(dy));
+    HIP(hipFree(dp));
+  }
+
   HIP(hipStreamDestroy(s));
   if (failures) {
     printf("%d check(s) failed\n", failures);
