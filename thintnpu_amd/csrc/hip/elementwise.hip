@@ -488,7 +488,14 @@ bool try_affine_flat(const thin_desc* x, const thin_desc* sc, const thin_desc* b
   // (a single small image): then more blocks shorten the launch.
   const uint32_t grid2 = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
   const bool nt = total * 16 >= kStreamingBytes;
-  if (nt)
+  // Views with gaps between images (the C2f narrowed x[:, C/2:]) read faster
+  // through cached loads, dense tensors through streaming loads
+  // ([32,64,80,80] view of [32,128,80,80]: 9.07 against 10.64 us; the full
+  // tensor: 17.9 against 18.9 us).
+  const bool gapped = x_row != 0 && x_row != span;
+  if (nt && gapped)
+    hipLaunchKernelGGL((affine_silu_flat_kernel<2, false, true>), dim3(grid2), dim3(kThreads), 0, stream, p);
+  else if (nt)
     hipLaunchKernelGGL((affine_silu_flat_kernel<2, true, true>), dim3(grid2), dim3(kThreads), 0, stream, p);
   else if (grid2 >= 256)
     hipLaunchKernelGGL((affine_silu_flat_kernel<2, false, false>), dim3(grid2), dim3(kThreads), 0, stream, p);
