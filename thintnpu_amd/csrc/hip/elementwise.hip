@@ -566,8 +566,12 @@ void launch_plan(const MapPlan<NIN>& p, bool vec, bool nt, hipStream_t stream) {
       const uint32_t grid = (p.units + kThreads * kUnroll - 1) / (kThreads * kUnroll);
       if (nt) hipLaunchKernelGGL((map_dense_kernel<T, V, NIN, kUnroll, true, Op>), dim3(grid), dim3(kThreads), 0,
                                  stream, p);
-      else hipLaunchKernelGGL((map_dense_kernel<T, V, NIN, kUnroll, false, Op>), dim3(grid), dim3(kThreads), 0,
-                              stream, p);
+      else if (grid >= 256)
+        hipLaunchKernelGGL((map_dense_kernel<T, V, NIN, kUnroll, false, Op>), dim3(grid), dim3(kThreads), 0,
+                           stream, p);
+      else  // small launches: one unit per thread, twice the blocks
+        hipLaunchKernelGGL((map_dense_kernel<T, V, NIN, 1, false, Op>), dim3((p.units + kThreads - 1) / kThreads),
+                           dim3(kThreads), 0, stream, p);
       return;
     }
   }
