@@ -139,8 +139,10 @@ thin_status launch_cat_group(const thin_desc* const* ins, int count, int dim, co
                              const int64_t* col_elems, int esize, bool nt, hipStream_t stream) {
   const bool stream_cfg = nt && sizeof(W) == 16;
   // one 16-byte vector per thread when streaming (C2f cat 4x[32,64,80,80]:
-  // 5.56 TB/s, against 5.40 with two and 5.24 with four)
-  const int U = stream_cfg ? 1 : 4;
+  // 5.56 TB/s, against 5.40 with two and 5.24 with four) and below the
+  // streaming size (4x[1,64,80,80]: 3.93 us, against 4.10 with two and 5.54
+  // with four); four for large cats of single elements
+  const int U = (stream_cfg || !nt) ? 1 : 4;
   const int64_t BS = stream_cfg ? kStreamThreads : kThreads;
   const int64_t wsize = sizeof(W);
   CatPlan p;
@@ -174,6 +176,8 @@ thin_status launch_cat_group(const thin_desc* const* ins, int count, int dim, co
   if (stream_cfg)
     hipLaunchKernelGGL((cat_kernel<W, 1, true, kStreamThreads>), dim3((uint32_t)total), dim3(kStreamThreads), 0,
                        stream, p);
+  else if (!nt)
+    hipLaunchKernelGGL((cat_kernel<W, 1, false, kThreads>), dim3((uint32_t)total), dim3(kThreads), 0, stream, p);
   else
     hipLaunchKernelGGL((cat_kernel<W, 4, false, kThreads>), dim3((uint32_t)total), dim3(kThreads), 0, stream, p);
   THIN_LAUNCH_CHECK("cat");
