@@ -300,9 +300,10 @@ thin_status launch_planes(const thin_desc* ins, const int32_t* up, int count, co
   if ((int64_t)units * 16 >= kStreamingBytes) {
     const uint32_t grid = grid_for(units, kStreamThreads, 2, 256u * 64u);
     hipLaunchKernelGGL((plane_kernel<2, true, kStreamThreads>), dim3(grid), dim3(kStreamThreads), 0, stream, p);
-  } else {
-    const uint32_t grid = grid_for(units, kThreads, 2, 256u * 64u);
-    hipLaunchKernelGGL((plane_kernel<2, false, kThreads>), dim3(grid), dim3(kThreads), 0, stream, p);
+  } else {  // below the streaming size one vector per thread: more blocks in flight
+    // (upsample [1,256,40,40]: 4.00 against 4.18 us with two)
+    const uint32_t grid = grid_for(units, kThreads, 1, 256u * 64u);
+    hipLaunchKernelGGL((plane_kernel<1, false, kThreads>), dim3(grid), dim3(kThreads), 0, stream, p);
   }
   THIN_LAUNCH_CHECK("plane");
   return THIN_OK;
