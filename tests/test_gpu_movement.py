@@ -344,6 +344,20 @@ def test_sppf_chain(gpu, n):
         check_pool(capi.sppf_nc1hwc0(x.to(gpu), 5, 3).cpu(), mv.sppf_blocked(x, 5, 3), f"packed zero={zero}")
 
 
+@pytest.mark.parametrize("n", [15, 16])
+def test_pool_block_forms(gpu, n):
+    """Under 256 (n, c1) planes a block pools one C0 half of a plane (n=15: 240
+    planes); from 256 on it pools all 16 lanes (n=16): both forms bit-exact,
+    with special values and +0/-0 ties, for the single pool and the SPPF chain."""
+    from thintnpu_amd import capi
+    x = pool_specials(to_blocked(normal16((n, 256, 7, 9), 71)))
+    check_pool(capi.maxpool_nc1hwc0(x.to(gpu), 5).cpu(), mv.maxpool_blocked(x, 5), f"n={n} maxpool k5")
+    check_pool(capi.sppf_nc1hwc0(x.to(gpu), 5, 3).cpu(), mv.sppf_blocked(x, 5, 3), f"n={n} sppf k5 x3")
+    for zero in (0.0, -0.0):
+        x = pool_specials_packed(to_blocked(normal16((n, 256, 6, 5), 72)), zero, 44)
+        check_pool(capi.sppf_nc1hwc0(x.to(gpu), 3, 2).cpu(), mv.sppf_blocked(x, 3, 2), f"n={n} packed zero={zero}")
+
+
 def test_sppf_large_planes_and_views(gpu):
     """A 40x40 plane (118 KB of LDS per block), a 64x64 plane (beyond one
     block's LDS: copy plus chained pools), a channel-block slice as x, and an

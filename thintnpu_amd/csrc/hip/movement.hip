@@ -698,7 +698,10 @@ constexpr size_t kSppfLdsBytes = 144 * 1024;
 // x3: 7.8 us at N=32 and 5.2 us at N=1, against 9.4 and 7.6 with 256)
 constexpr uint32_t kSppfThreads = 1024;
 
-template <int K, bool NT, uint32_t BS>
+// VPP: 16-byte vectors per pixel held by a block.  2: the block pools all 16
+// C0 lanes of its plane; 1: one C0 half (lanes 0-7 or 8-15, block parity), so
+// that a small batch launches twice the blocks (channels pool independently).
+template <int K, bool NT, uint32_t BS, uint32_t VPP>
 __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
   constexpr int R = K / 2;
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -706,7 +709,8 @@ __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
   typedef PoolVec<_Float16, 8> PV;
   extern __shared__ __attribute__((aligned(16))) char sppf_lds[];
   __shared__ uint32_t wave_zero_signs[BS / 64];
-  const uint32_t plane = blockIdx.x;
+  const uint32_t plane = VPP == 2 ? blockIdx.x : blockIdx.x >> 1;
+  const uint32_t half = VPP == 2 ? 0u : (blockIdx.x & 1u) * 8u;  // C0 lane offset
   const uint32_t n = p.div_c1.div(plane), c = plane - n * p.c1;
   const uint32_t row_vecs = p.div_row.d, prow = p.div_prow.d;
   const uint32_t prows = p.h + 2 * R;
@@ -716,24 +720,24 @@ __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
   PV ninf;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ninf.e[j] = (_Float16)(-__builtin_inff());
-  const _Float16* xp = p.x + n * p.xs[0] + c * p.xs[1];
-  auto slot = [&](uint32_t r) { return p.y + n * p.ys[0] + ((r - p.pool_only) * p.c1 + c) * p.ys[1]; };
+  const _Float16* xp = p.x + n * p.xs[0] + c * p.xs[1] + half;
+  auto slot = [&](uint32_t r) { return p.y + n * p.ys[0] + ((r - p.pool_only) * p.c1 + c) * p.ys[1] + half; };
   // stage the padded plane; copy x to output slot 0
   u16x8 min_pos = (u16x8)(uint16_t)0xffff, min_neg = (u16x8)(uint16_t)0xffff;
   _Float16* y0 = p.pool_only ? nullptr : slot(0);
   for (uint32_t i = threadIdx.x; i < tile; i += BS) {
     const uint32_t rr = p.div_prow.div(i), k = i - rr * prow;
-    const int xx = (int)(k >> 1) - R, yy = (int)rr - R;
+    const int xx = (int)(k / VPP) - R, yy = (int)rr - R;
     PV v = ninf;
     if (yy >= 0 && yy < (int)p.h && xx >= 0 && xx < (int)p.w) {
-      const int64_t off = (int64_t)yy * p.xs[2] + (int64_t)xx * 16 + (k & 1u) * 8;
+      const int64_t off = (int64_t)yy * p.xs[2] + (int64_t)xx * 16 + (VPP == 2 ? (k & 1u) * 8 : 0u);
       v = *reinterpret_cast<const PV*>(xp + off);
       const u16x8 b = __builtin_bit_cast(u16x8, v);
       min_pos = __builtin_elementwise_min(min_pos, b);
       min_neg = __builtin_elementwise_min(min_neg, b ^ (uint16_t)0x8000);
       if (!p.pool_only) {
         const h8 hv = __builtin_bit_cast(h8, v);
-        h8* dst = reinterpret_cast<h8*>(y0 + (int64_t)yy * p.ys[2] + (int64_t)xx * 16 + (k & 1u) * 8);
+        h8* dst = reinterpret_cast<h8*>(y0 + (int64_t)yy * p.ys[2] + (int64_t)xx * 16 + (VPP == 2 ? (k & 1u) * 8 : 0u));
         if constexpr (NT) __builtin_nontemporal_store(hv, dst);
         else *dst = hv;
       }
@@ -758,12 +762,12 @@ __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
         const h8* ih = reinterpret_cast<const h8*>(in);
         h8 m = ih[base];
 #pragma unroll
-        for (int j = 1; j <= 2 * R; ++j) m = __builtin_elementwise_maximum(m, ih[base + 2 * j]);
+        for (int j = 1; j <= 2 * R; ++j) m = __builtin_elementwise_maximum(m, ih[base + VPP * j]);
         reinterpret_cast<h8*>(hm)[i] = m;
       } else {
         PV m = ninf;
 #pragma unroll
-        for (int j = 0; j <= 2 * R; ++j) keep_max(m, in[base + 2 * j]);
+        for (int j = 0; j <= 2 * R; ++j) keep_max(m, in[base + VPP * j]);
         hm[i] = m;
       }
     }
@@ -783,9 +787,9 @@ __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
 #pragma unroll
         for (int dy = 0; dy <= 2 * R; ++dy) keep_max(m, hm[(r + dy) * row_vecs + k]);
       }
-      in[(r + R) * prow + k + 2 * R] = m;  // the next repeat's input
+      in[(r + R) * prow + k + VPP * R] = m;  // the next repeat's input
       const h8 hv = __builtin_bit_cast(h8, m);
-      h8* dst = reinterpret_cast<h8*>(yr + (int64_t)r * p.ys[2] + (int64_t)(k >> 1) * 16 + (k & 1u) * 8);
+      h8* dst = reinterpret_cast<h8*>(yr + (int64_t)r * p.ys[2] + (int64_t)(k / VPP) * 16 + (VPP == 2 ? (k & 1u) * 8 : 0u));
       if constexpr (NT) __builtin_nontemporal_store(hv, dst);
       else *dst = hv;
     }
@@ -814,16 +818,22 @@ thin_status launch_sppf(const thin_desc* x, int32_t kernel, int32_t repeats, boo
   p.repeats = (uint32_t)repeats;
   p.pool_only = pool_only ? 1u : 0u;
   p.div_c1 = FastDiv::make((uint32_t)C1);
-  p.div_row = FastDiv::make((uint32_t)(W * 2));
-  p.div_prow = FastDiv::make((uint32_t)((W + 2 * R) * 2));
+  // fewer than 256 planes: one block per C0 half of a plane
+  // ([1,256,20,20] k5 x3 + cat: see the SPPF row of the kernel notes)
+  const bool split = N * C1 < 256;
+  const int64_t vpp = split ? 1 : 2;
+  p.div_row = FastDiv::make((uint32_t)(W * vpp));
+  p.div_prow = FastDiv::make((uint32_t)((W + 2 * R) * vpp));
   const bool nt = numel(out) * 2 >= kStreamingBytes;
-  const uint32_t blocks = (uint32_t)(N * C1);
+  const uint32_t blocks = (uint32_t)(N * C1 * (split ? 2 : 1));
   switch (kernel) {
 #define THIN_SPPF(KK)                                                                                        \
   case KK:                                                                                                   \
-    if (nt) hipLaunchKernelGGL((sppf_kernel<KK, true, kSppfThreads>), dim3(blocks), dim3(kSppfThreads),      \
-                               lds, stream, p);                                                      \
-    else hipLaunchKernelGGL((sppf_kernel<KK, false, kSppfThreads>), dim3(blocks), dim3(kSppfThreads),        \
+    if (split) hipLaunchKernelGGL((sppf_kernel<KK, false, kSppfThreads, 1>), dim3(blocks), dim3(kSppfThreads), \
+                                  lds, stream, p);                                                   \
+    else if (nt) hipLaunchKernelGGL((sppf_kernel<KK, true, kSppfThreads, 2>), dim3(blocks), dim3(kSppfThreads), \
+                                    lds, stream, p);                                                 \
+    else hipLaunchKernelGGL((sppf_kernel<KK, false, kSppfThreads, 2>), dim3(blocks), dim3(kSppfThreads),     \
                             lds, stream, p);                                                         \
     break;
     THIN_SPPF(1) THIN_SPPF(3) THIN_SPPF(5) THIN_SPPF(7) THIN_SPPF(9) THIN_SPPF(11) THIN_SPPF(13) THIN_SPPF(15)
