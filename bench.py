@@ -109,8 +109,8 @@ def time_launches(launch, sets, iters, rounds=5):
 # copy map_dense_kernel<OpCopy> over the same [32,8,80,80,16] fp16 tensor
 # (104857600 B read + written), from `bench.py --profile dominant|copy --iters 20`
 # (profiles/affine_silu_flat_n32_128x80x80_pmc.md).
-PMC_KIB = {"dominant": {"FETCH_SIZE": 25622.0, "WRITE_SIZE": 51200.25},
-           "copy": {"FETCH_SIZE": 25610.0, "WRITE_SIZE": 51250.625}}
+PMC_KIB = {"dominant": {"FETCH_SIZE": 25622.0, "WRITE_SIZE": 51200.0},
+           "copy": {"FETCH_SIZE": 25610.0, "WRITE_SIZE": 51253.625}}
 COPY_BYTES_EACH_WAY = 52428800
 
 
