@@ -504,6 +504,7 @@ void launch_rows(const SoftmaxPlan& p, int64_t chunks, uint64_t rows, hipStream_
   else if (chunks <= 8) THIN_ROWG(4, 2);
   else if (chunks <= 16) THIN_ROWG(8, 2);
   else if (chunks <= 32) THIN_ROWG(16, 2);
+  else if (chunks <= 64 && grid(32) < 256) THIN_ROWG(64, 1);  // few rows: one row per wave, more waves
   else if (chunks <= 64) THIN_ROWG(32, 2);
   else if (chunks <= 128) THIN_ROWG(64, 2);
   else if (chunks <= 256) THIN_ROWG(64, 4);
