@@ -110,7 +110,7 @@ def time_launches(launch, sets, iters, rounds=5):
 # (104857600 B read + written), from `bench.py --profile dominant|copy --iters 20`
 # (profiles/affine_silu_flat_n32_128x80x80_pmc.md).
 PMC_KIB = {"dominant": {"FETCH_SIZE": 25622.0, "WRITE_SIZE": 51200.0},
-           "copy": {"FETCH_SIZE": 25610.0, "WRITE_SIZE": 51253.625}}
+           "copy": {"FETCH_SIZE": 25610.0, "WRITE_SIZE": 51257.25}}
 COPY_BYTES_EACH_WAY = 52428800
 
 
