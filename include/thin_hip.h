@@ -263,6 +263,26 @@ thin_status thin_detection_select(const thin_desc* decoded, int64_t max_det, int
                                   void* out, void* workspace, size_t workspace_bytes,
                                   const thin_select_trace* trace, hipStream_t stream);
 
+/* Capacity of the static device scratch behind thin_detection_select_noalloc
+ * (8 MiB per GPU the library runs on, held until the process ends; the C5
+ * shape [1,8400,84] with K = 300 needs about 100 KB per image). */
+#define THIN_SELECT_SCRATCH_BYTES (8u << 20)
+
+/* thin_detection_select without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: the
+ * reference allocates its intermediates per call.  Same arguments, results
+ * and errors as thin_detection_select; the intermediates live in a static
+ * device array of the library, one per GPU, whose device address is taken
+ * once per device on the first call with that device current.  Calls whose
+ * thin_detection_select_workspace(...) exceeds THIN_SELECT_SCRATCH_BYTES fail
+ * with THIN_ERR_WORKSPACE.  Allocates nothing (no hipMalloc, hipFree or
+ * allocating library call).  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (two streams, or two host threads) race and
+ * must be ordered by the caller. */
+thin_status thin_detection_select_noalloc(const thin_desc* decoded, int64_t max_det, int32_t agnostic,
+                                          void* out, const thin_select_trace* trace, hipStream_t stream);
+
 /* ------------------------------------------------------------------ */
 /* Attention contractions                                              */
 /* ------------------------------------------------------------------ */

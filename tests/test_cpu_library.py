@@ -45,6 +45,9 @@ def test_every_declaration_cites_the_reference():
             continue
         start = text.index(name + "(")
         comment = text[text.rfind("/*", 0, start):start]
+        if "No counterpart in the reference" in comment:
+            assert "cannot allocate" in " ".join(comment.replace("*", " ").split()), name  # the allocation-free variant names its callers
+            continue
         assert re.search(r"\w+\.(cpp|py|h):\d+", comment), name
 
 

@@ -20,6 +20,7 @@ MAX_DIMS = 8
 MAX_CAT_INPUTS = 64
 
 F16, F32, I64, I32, I16, U8, F64, BF16 = range(8)
+SELECT_SCRATCH_BYTES = 8 << 20  # THIN_SELECT_SCRATCH_BYTES of include/thin_hip.h
 SUB, MUL, DIV, ADD = 0, 1, 2, 3
 SIGMOID, SILU = 0, 1
 
@@ -95,6 +96,7 @@ def lib() -> ctypes.CDLL:
             "thin_detect_decode": [P, P, ctypes.POINTER(i32), ctypes.POINTER(f64), i32, i32, P, vp],
             "thin_detection_select": [P, i64, i32, vp, vp, ctypes.c_size_t,
                                       ctypes.POINTER(ThinSelectTrace), vp],
+            "thin_detection_select_noalloc": [P, i64, i32, vp, ctypes.POINTER(ThinSelectTrace), vp],
             "thin_layout_bmm_shape": [P, P, ctypes.POINTER(ThinBmmLayout), ctypes.POINTER(i32),
                                       ctypes.POINTER(i64)],
             "thin_layout_bmm": [P, P, ctypes.POINTER(ThinBmmLayout), P, vp],
@@ -326,14 +328,19 @@ def detection_select_workspace(b: int, a: int, nc: int, max_det: int, agnostic: 
 
 
 def detection_select(decoded, max_det: int, agnostic: bool = False, trace: bool = False,
-                     stream=None, out=None, workspace=None):
+                     stream=None, out=None, workspace=None, noalloc: bool = False):
+    """thin_detection_select with a workspace (given, or allocated here), or,
+    with noalloc=True, thin_detection_select_noalloc on the library's static
+    scratch (no workspace argument)."""
     b, a, ch = decoded.shape
     nc = ch - 4
     k = min(max_det, a)
     dev = decoded.device
     out = torch.empty((b, k, 6), dtype=torch.float32, device=dev) if out is None else out
-    ws_bytes = detection_select_workspace(b, a, nc, max_det, agnostic)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if workspace is None else workspace
+    ws = None
+    if not noalloc:
+        ws_bytes = detection_select_workspace(b, a, nc, max_det, agnostic)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if workspace is None else workspace
     tr = None
     tensors = None
     if trace:
@@ -347,9 +354,14 @@ def detection_select(decoded, max_det: int, agnostic: bool = False, trace: bool 
             labels=torch.empty((b, k), dtype=torch.int64, device=dev),
         )
         tr = ThinSelectTrace(**{n: (t.data_ptr() if t.numel() else None) for n, t in tensors.items()})
-    _call("thin_detection_select", _ref(desc(decoded)), max_det, int(agnostic),
-          out.data_ptr() if out.numel() else None, ws.data_ptr(), ws.numel(),
-          ctypes.byref(tr) if tr is not None else None, _stream(stream))
+    trace_arg = ctypes.byref(tr) if tr is not None else None
+    out_ptr = out.data_ptr() if out.numel() else None
+    if noalloc:
+        _call("thin_detection_select_noalloc", _ref(desc(decoded)), max_det, int(agnostic), out_ptr, trace_arg,
+              _stream(stream))
+    else:
+        _call("thin_detection_select", _ref(desc(decoded)), max_det, int(agnostic), out_ptr, ws.data_ptr(),
+              ws.numel(), trace_arg, _stream(stream))
     if trace:
         return out, tensors
     return out

@@ -18,6 +18,8 @@
 
 #include <string.h>
 
+#include <mutex>
+
 namespace thin {
 namespace {
 
@@ -765,10 +767,15 @@ extern "C" size_t thin_detection_select_workspace(int64_t batches, int64_t ancho
   return ws_layout(batches, anchors, classes, max_det, agnostic != 0).total;
 }
 
-extern "C" thin_status thin_detection_select(const thin_desc* decoded, int64_t max_det, int32_t agnostic, void* out,
-                                             void* workspace, size_t workspace_bytes,
-                                             const thin_select_trace* trace, hipStream_t stream) {
-  clear_error();
+namespace thin {
+namespace {
+
+// Argument checks shared by both entry points.  Sets *skip when the call has
+// nothing to launch (empty batch or anchors, or K == 0 without a class_max
+// trace: selection_flow.cpp:436-439).
+thin_status select_validate(const thin_desc* decoded, int64_t max_det, void* out, const thin_select_trace* trace,
+                            bool* skip) {
+  *skip = false;
   THIN_REQUIRE(desc_valid(decoded), THIN_ERR_INVALID, "detection_select: invalid descriptor");
   THIN_REQUIRE(decoded->dtype == THIN_F16 && decoded->rank == 3, THIN_ERR_INVALID,
                "detection_select expects float16 [B,A,4+nc]");
@@ -776,18 +783,23 @@ extern "C" thin_status thin_detection_select(const thin_desc* decoded, int64_t m
                "detection_select requires nc > 0 and max_det >= 0");
   const int64_t B = decoded->sizes[0], A = decoded->sizes[1], nc = decoded->sizes[2] - 4;
   const int64_t K = max_det < A ? max_det : A;
-  // With K == 0 only a requested class_max trace has work (selection_flow.cpp:439).
-  if (B == 0 || A == 0 || (K == 0 && !(trace && trace->class_max))) return THIN_OK;
+  if (B == 0 || A == 0 || (K == 0 && !(trace && trace->class_max))) {
+    *skip = true;
+    return THIN_OK;
+  }
   THIN_REQUIRE(out != nullptr || K == 0, THIN_ERR_INVALID, "detection_select: null output");
   THIN_REQUIRE(A < ((int64_t)1 << 31) && K * nc < ((int64_t)1 << 31), THIN_ERR_UNSUPPORTED,
                "detection_select: candidate count exceeds 2^31");
-  const bool agn = agnostic != 0;
-  const WsLayout w = ws_layout(B, A, nc, max_det, agn);
-  THIN_REQUIRE(workspace != nullptr && workspace_bytes >= w.total, THIN_ERR_WORKSPACE,
-               "detection_select: workspace of %zu bytes needed, %zu given", w.total, workspace_bytes);
-  THIN_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, THIN_ERR_WORKSPACE,
-               "detection_select: workspace must be 256-byte aligned");
-  char* ws = static_cast<char*>(workspace);
+  return THIN_OK;
+}
+
+// Enqueues the selection kernels over a validated call; `ws` holds w.total
+// bytes, 256-byte aligned.  Every workspace region is written before it is
+// read within the call, so no region needs clearing.
+thin_status select_run(const thin_desc* decoded, int64_t max_det, bool agn, void* out, char* ws, const WsLayout& w,
+                       const thin_select_trace* trace, hipStream_t stream) {
+  const int64_t B = decoded->sizes[0], A = decoded->sizes[1], nc = decoded->sizes[2] - 4;
+  const int64_t K = max_det < A ? max_det : A;
   uint16_t* bits1 = reinterpret_cast<uint16_t*>(ws + w.bits1);
   int32_t* cls1 = reinterpret_cast<int32_t*>(ws + w.cls1);
   int32_t* stage1 = reinterpret_cast<int32_t*>(ws + w.stage1);
@@ -868,4 +880,76 @@ extern "C" thin_status thin_detection_select(const thin_desc* decoded, int64_t m
   hipLaunchKernelGGL(pack_kernel, dim3(blocks_for((uint64_t)(B * K))), dim3(kThreads), 0, stream, pa);
   THIN_LAUNCH_CHECK("pack");
   return THIN_OK;
+}
+
+}  // namespace
+}  // namespace thin
+
+extern "C" thin_status thin_detection_select(const thin_desc* decoded, int64_t max_det, int32_t agnostic, void* out,
+                                             void* workspace, size_t workspace_bytes,
+                                             const thin_select_trace* trace, hipStream_t stream) {
+  clear_error();
+  bool skip = false;
+  thin_status s = select_validate(decoded, max_det, out, trace, &skip);
+  if (s != THIN_OK || skip) return s;
+  const bool agn = agnostic != 0;
+  const WsLayout w = ws_layout(decoded->sizes[0], decoded->sizes[1], decoded->sizes[2] - 4, max_det, agn);
+  THIN_REQUIRE(workspace != nullptr && workspace_bytes >= w.total, THIN_ERR_WORKSPACE,
+               "detection_select: workspace of %zu bytes needed, %zu given", w.total, workspace_bytes);
+  THIN_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, THIN_ERR_WORKSPACE,
+               "detection_select: workspace must be 256-byte aligned");
+  return select_run(decoded, max_det, agn, out, static_cast<char*>(workspace), w, trace, stream);
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+// The workspace of thin_detection_select_noalloc lives in a static device
+// array of this library (one copy per GPU, held until the process ends).  In
+// host code `scratch` names a host-side shadow, not device memory: its device
+// address comes from hipGetSymbolAddress, taken once per device on the first
+// call with that device current, and only that address reaches the kernels.
+namespace thin {
+namespace {
+
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) unsigned char scratch[THIN_SELECT_SCRATCH_BYTES];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kScratchDevices];
+
+thin_status scratch_address(void** addr) {
+  int device = -1;
+  THIN_HIP_CHECK(hipGetDevice(&device));
+  THIN_REQUIRE(device >= 0 && device < kScratchDevices, THIN_ERR_UNSUPPORTED,
+               "detection_select_noalloc: device index %d beyond %d", device, kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_addr[device]) {
+    void* p = nullptr;
+    THIN_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    THIN_REQUIRE(p != nullptr && reinterpret_cast<uintptr_t>(p) % 256 == 0, THIN_ERR_HIP,
+                 "detection_select_noalloc: scratch address %p is not 256-byte aligned", p);
+    g_scratch_addr[device] = p;
+  }
+  *addr = g_scratch_addr[device];
+  return THIN_OK;
+}
+
+}  // namespace
+}  // namespace thin
+
+extern "C" thin_status thin_detection_select_noalloc(const thin_desc* decoded, int64_t max_det, int32_t agnostic,
+                                                     void* out, const thin_select_trace* trace, hipStream_t stream) {
+  clear_error();
+  bool skip = false;
+  thin_status s = select_validate(decoded, max_det, out, trace, &skip);
+  if (s != THIN_OK || skip) return s;
+  const bool agn = agnostic != 0;
+  const WsLayout w = ws_layout(decoded->sizes[0], decoded->sizes[1], decoded->sizes[2] - 4, max_det, agn);
+  THIN_REQUIRE(w.total <= (size_t)THIN_SELECT_SCRATCH_BYTES, THIN_ERR_WORKSPACE,
+               "detection_select_noalloc: these sizes need %zu bytes of scratch, the static scratch holds %zu "
+               "(use thin_detection_select with a workspace)",
+               w.total, (size_t)THIN_SELECT_SCRATCH_BYTES);
+  void* ws = nullptr;
+  s = scratch_address(&ws);
+  if (s != THIN_OK) return s;
+  return select_run(decoded, max_det, agn, out, static_cast<char*>(ws), w, trace, stream);
 }
