@@ -5,7 +5,8 @@ the same seeded inputs (verify_ops.py:74, verify_strided_binary.py:18-57,
 verify_all.py:76-81); these functions are those CPU op sequences.
 
 Pinning (tests/test_oracle_elementwise.py):
-  binary_*      -- bit-exact against float64 numpy evaluation rounded once to
+  binary_*      -- (binary, binary_scalar, binary_scalar_rounded)
+                   bit-exact against float64 numpy evaluation rounded once to
                    fp16 (exact sums/products; division double rounding is
                    innocuous at 53 >= 2*11+2), i.e. the correctly rounded result.
   sigmoid/silu  -- within 1 fp16 ulp of a float64 evaluation; NaN/inf cases.
@@ -59,6 +60,16 @@ def binary_scalar(op: int, x: torch.Tensor, scalar: float, scalar_first: bool = 
     if name in ("add", "sub"):
         return getattr(torch, name)(x, scalar, alpha=alpha)
     return getattr(torch, name)(x, scalar)
+
+
+def binary_scalar_rounded(op: int, x: torch.Tensor, scalar: float, scalar_first: bool = False,
+                          alpha: float = 1.0) -> torch.Tensor:
+    """Tensor op Python number by the reference's rule: the 0-d CPU operand is
+    converted to the tensor dtype first (ops.cpp:466-467), then the
+    tensor-tensor op runs (ops.cpp:468-497).  That is binary() against a
+    broadcast tensor holding the rounded scalar."""
+    s = torch.full_like(x, scalar)
+    return binary(op, s, x, alpha) if scalar_first else binary(op, x, s, alpha)
 
 
 def sigmoid(x: torch.Tensor) -> torch.Tensor:

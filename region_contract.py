@@ -1,23 +1,28 @@
 """RegionContract: the frozen-state contract a FrozenGraph pilot validates.
 
-Same API as the reference's region_contract.py:5-28.  Construction checks that
-every parameter and buffer of the region is a fixed fp16 ``npu`` inference
-tensor with a version counter (prepared under ``no_grad()``, not
-``inference_mode()``), then hands the modules to the native ``Guard``
-(thintnpu_amd/csrc/torch/region_guard.cpp), whose ``validate()`` raises
-ValueError on any drift: module class/dict, training mode, hooks, children,
-forward bindings (except ``ignored_forward`` modules, whose forward the pilot
-swaps itself), the operator attributes below, and parameter/buffer identity,
-version, storage, shape, dtype and device.
+The drop-in for the reference's region_contract.py:5-28. It has the same
+constructor `RegionContract(roots, ignored_forward=())`, the same `attributes`
+table and the same `validate()`. Both halves are native
+(thintnpu_amd/csrc/torch/region_guard.cpp -> thin_backend/_region_guard*.so):
+
+* `require_frozen_fp16` admits the region. Every parameter and buffer must be
+  a version-counted (no_grad, not inference_mode) fp16 npu tensor without
+  gradient. Anything else raises ValueError.
+* `Guard` snapshots every module of the region. Its `validate()` raises
+  ValueError on any drift a captured graph could not see:
+  - class, `__dict__`, training mode, hooks, children;
+  - forward bindings, except the modules in `ignored_forward`, whose forward
+    the pilot swaps itself;
+  - the operator attributes below;
+  - parameter and buffer identity, version, storage and metadata.
 """
-import torch
+import thin_backend  # noqa: F401  (loads the npu device the parameters live on)
+from thin_backend._region_guard import Guard, require_frozen_fp16
 
-import thin_backend  # noqa: F401  (the npu device and the guard extension live there)
-from thin_backend._region_guard import Guard
-
-# Operator-configuration attributes frozen by the guard (the reference's list:
-# nn.Conv2d / Upsample / MaxPool2d, Ultralytics Bottleneck / C2f / Attention /
-# Detect fields, and the attributes the blocked rewrite sets).
+# Operator-configuration attributes the guard freezes. Pilots and their tests
+# key on this table: nn.Conv2d / Upsample / MaxPool2d fields, Ultralytics
+# Bottleneck / C2f / Attention / Detect fields, and the attributes the blocked
+# rewrite sets.
 ATTRIBUTES = ('in_channels', 'out_channels', 'kernel_size', 'stride', 'padding', 'padding_mode',
               'dilation', 'groups', 'add', 'c', 'inplace', 'scale_factor', 'mode',
               'align_corners', 'size', 'ceil_mode', 'return_indices',
@@ -30,18 +35,9 @@ class RegionContract:
     attributes = ATTRIBUTES
 
     def __init__(self, roots, ignored_forward=()):
-        modules = [m for root in roots for m in root.modules()]
-        for module in modules:
-            for tensor in (*module._parameters.values(), *module._buffers.values()):
-                if tensor is None:
-                    continue
-                try:
-                    tensor._version
-                except RuntimeError as error:
-                    raise ValueError('Prepare versioned parameters under no_grad(), not inference_mode()') from error
-                if tensor.requires_grad or tensor.dtype != torch.float16 or tensor.device.type != 'npu':
-                    raise ValueError('Expected fixed FP16 NPU inference parameters')
-        self.guard = Guard(modules, set(ignored_forward), self.attributes)
+        region = [module for root in roots for module in root.modules()]
+        require_frozen_fp16(region)
+        self.guard = Guard(region, set(ignored_forward), self.attributes)
 
     def validate(self):
         self.guard.validate()

@@ -5,7 +5,9 @@ reference's verify_ops.py, verify_graph.py, verify_aten.py, verify_all.py,
 verify_cat_plan.py, verify_dfl_softmax.py and verify_selection_flow.py device
 checks.  Values are compared with the same CPU oracle as the C-ABI tests."""
 import math
+import os
 import threading
+from pathlib import Path
 
 import pytest
 import torch
@@ -16,7 +18,9 @@ from oracle import movement as mv
 from oracle import reductions as rd
 from oracle import selection as sel
 from oracle.numerics import assert_rel, assert_ulp, bits_equal
-from tests.helpers import gen, normal16, random_bits16, to_blocked
+from tests.helpers import gen, normal16, random_bits16, specials16, to_blocked
+
+ROOT = Path(__file__).resolve().parent.parent
 
 pytestmark = pytest.mark.gpu
 
@@ -223,6 +227,96 @@ def test_frozen_graph(npu):
         g.close()
 
 
+def test_runtime_graph_phases(npu):
+    """thin_backend::RuntimeGraph refuses calls out of phase (empty ->
+    recording -> executable -> closed) and stays usable for what is legal."""
+    with torch.inference_mode():
+        x = torch.linspace(-1, 1, 1024).to(npu)
+        g = torch.classes.thin_backend.RuntimeGraph()
+        with pytest.raises(RuntimeError, match="nothing to replay"):
+            g.replay()
+        with pytest.raises(RuntimeError, match="not recording"):
+            g.end()
+        g.begin()
+        with pytest.raises(RuntimeError, match="records exactly once"):
+            g.begin()
+        y = torch.sigmoid(x)
+        g.end()
+        with pytest.raises(RuntimeError, match="records exactly once"):
+            g.begin()
+        g.replay()
+        eager = torch.sigmoid(x).cpu()
+        assert torch.equal(y.cpu(), eager)
+        g.close()
+        g.close()
+        with pytest.raises(RuntimeError, match="closed"):
+            g.replay()
+        # a graph closed while recording discards the recording
+        h = torch.classes.thin_backend.RuntimeGraph()
+        h.begin()
+        torch.sigmoid(x)
+        h.close()
+        assert torch.equal(torch.sigmoid(x).cpu(), eager)
+
+
+def test_cross_thread_free_and_reuse(npu):
+    """A block released by one host thread while another thread's stream
+    could still read it must not be handed out again under that read.  Thread
+    B computes sigmoid of a tensor that only B holds, then drops it; thread A
+    at once allocates blocks of the same size on its own stream and
+    overwrites them.  B's result must equal the oracle.  Eager ops finish
+    before they return, as the reference's do (backend.cpp:46)."""
+    x = random_bits16((1 << 24,), 88)          # 32 MB: a launch long enough to overlap
+    with torch.inference_mode():
+        expect = torch.sigmoid(x.to(npu)).cpu()  # the same kernel, one thread
+        assert_ulp(expect, ew.sigmoid(x), 2)
+        held = [x.to(npu)]                     # allocated on this thread's stream
+        done = threading.Event()
+        result = {}
+
+        def reader():
+            t = held.pop()
+            y = torch.sigmoid(t)
+            del t                              # the only reference: the block is released here
+            result["y"] = y
+            done.set()
+
+        b = threading.Thread(target=reader)
+        b.start()
+        done.wait(60)
+        junk = [torch.empty(1 << 24, dtype=torch.float16, device=npu).fill_(7.0) for _ in range(3)]
+        b.join()
+        assert "y" in result
+        assert bits_equal(result["y"].cpu(), expect)
+        assert all(bool((j.cpu() == 7.0).all()) for j in junk)
+
+
+def test_async_mode_is_single_threaded(npu, tmp_path):
+    """THIN_ASYNC=1 leaves eager ops asynchronous for one host thread; a
+    second thread that touches the device raises instead of racing."""
+    import subprocess
+    import sys
+    script = tmp_path / "async_probe.py"
+    script.write_text(
+        "import sys, threading, torch\n"
+        f"sys.path.insert(0, {str(ROOT)!r})\n"
+        "import thin_backend\n"
+        "x = torch.linspace(-1, 1, 4096).to('npu')\n"
+        "assert torch.equal((x + x).cpu(), x.cpu() + x.cpu())\n"
+        "err = []\n"
+        "def other():\n"
+        "    try:\n"
+        "        torch.sigmoid(x)\n"
+        "    except RuntimeError as e:\n"
+        "        err.append(str(e))\n"
+        "t = threading.Thread(target=other); t.start(); t.join()\n"
+        "assert err and 'THIN_ASYNC=1' in err[0], err\n"
+        "print('async-probe-ok')\n")
+    env = dict(os.environ, THIN_ASYNC="1")
+    out = subprocess.run([sys.executable, str(script)], env=env, capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0 and "async-probe-ok" in out.stdout, out.stderr[-2000:]
+
+
 def test_cat_plan_capture_changed_input(npu):
     """verify_cat_plan.py:42-50: split -> cat captured, replayed with new inputs."""
     from thin_backend.graph import CapturedForward
@@ -235,6 +329,27 @@ def test_cat_plan_capture_changed_input(npu):
                     changed = x * scale
                     assert bits_equal(graph(changed.to(npu)).cpu(), changed)
                 graph.close()
+
+
+def test_scalar_operand_rounded_to_tensor_dtype(npu):
+    """A 0-d CPU operand is converted to the tensor's dtype before the op, as
+    the reference converts it (ops.cpp:466-467): C2PSA's q * key_dim**-0.5
+    (whole_blocked.py:97) multiplies by the fp16 value of 1/sqrt(32).  The
+    input draws enough values that PyTorch CPU's fp32-scalar rule gives
+    different bits on some of them, so the check tells the rules apart."""
+    x = torch.cat([random_bits16((200_000,), 77), specials16()])
+    scale = 32 ** -0.5
+    with torch.inference_mode():
+        d = x.to(npu)
+        for op, name in ((1, "mul"), (2, "div"), (3, "add"), (0, "sub")):
+            got = getattr(torch, name)(d, scale).cpu()
+            assert bits_equal(got, ew.binary_scalar_rounded(op, x, scale)), name
+            if name in ("add", "sub"):
+                continue
+            got_first = getattr(torch, name)(torch.tensor(scale, dtype=torch.float64), d).cpu()
+            assert bits_equal(got_first, ew.binary_scalar_rounded(op, x, scale, True)), name + " first"
+        assert bits_equal((d * scale).cpu(), ew.binary_scalar_rounded(1, x, scale))
+        assert not bits_equal((d * scale).cpu(), ew.binary_scalar(1, x, scale))
 
 
 def test_strided_binary_eager_equals_capture(npu):
@@ -633,7 +748,7 @@ def test_attention_block_flow(npu):
         out = mixed + position
     q_cpu = qkv_blocked.view(batch, -1, tokens, 16)
     assert bits_equal(selected.cpu(), ob.channel_select(q_cpu, heads, 0, key_dim))
-    assert bits_equal(query.cpu(), ew.binary_scalar(1, selected.cpu(), scale))
+    assert bits_equal(query.cpu(), ew.binary_scalar_rounded(1, selected.cpu(), scale))
     assert scores.shape == (heads, tokens, tokens)
     assert bits_equal(scores.cpu(), ob.layout_bmm(query.cpu(), q_cpu, True, False, False, heads, 0, key_dim,
                                                   key_dim, key_dim))

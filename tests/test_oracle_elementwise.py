@@ -64,6 +64,28 @@ def test_scalar_rules():
             assert rep["nan_match"] and rep["max_ulp"] == 0, (op, first, sc, rep)
 
 
+def test_scalar_rounded_rule():
+    """The reference's rule: the scalar is rounded to fp16 for every op, then
+    each op is one correctly rounded fp16 operation on fp16 values.  1/sqrt(32)
+    is not an fp16 value, so this rule and PyTorch CPU's fp32 rule for mul
+    must disagree on some inputs (the check would pass either way otherwise)."""
+    x = random_bits16((8_000,), 14)
+    x64 = x.double().numpy()
+    for sc in (0.17677669529663687, 0.3, 3.0):
+        s16 = np.float64(np.float16(sc))
+        with np.errstate(all="ignore"):
+            models = {(3, False): x64 + s16, (0, False): x64 - s16, (0, True): s16 - x64, (3, True): s16 + x64,
+                      (1, False): x64 * s16, (1, True): s16 * x64, (2, False): x64 / s16, (2, True): s16 / x64}
+        for (op, first), ex in models.items():
+            ref = torch.from_numpy(np.float32(ex).astype(np.float16))
+            rep = ulp_report(ew.binary_scalar_rounded(op, x, sc, first), ref)
+            assert rep["nan_match"] and rep["max_ulp"] == 0, (op, first, sc, rep)
+    q = ew.binary_scalar_rounded(1, x, 32 ** -0.5)
+    cpu = ew.binary_scalar(1, x, 32 ** -0.5)
+    finite = torch.isfinite(q.float()) & torch.isfinite(cpu.float())
+    assert (q[finite] != cpu[finite]).any()
+
+
 def test_unary_oracles_within_one_ulp_of_float64():
     x = torch.cat([random_bits16((100_000,), 3), specials16()])
     x64 = x.double().numpy()

@@ -1,28 +1,80 @@
-"""Fixed-shape capture/replay on the backend's hipGraph RuntimeGraph.
+"""Capture one fixed-shape inference forward into a hipGraph and replay it.
 
-Same contract as the reference's thin_backend/graph.py:6-51: warmup, capture
-of one forward into a graph with graph-owned workspace and borrowed outputs,
-input metadata checks, replay on the creating thread only.
+`CapturedForward(forward, example, warmup=3)` is the drop-in for the
+reference's thin_backend/graph.py:6-51: the same constructor, the same
+`replay()`, `__call__(value)`, `close()` and `outputs`, and the same exception
+types and messages.
+
+How this one works:
+
+* The graph reads its input from one static device tensor, `input`. It is
+  allocated with the example's layout and filled from the example.
+* `forward` runs `warmup` times eagerly first. This lets the caching allocator
+  hold the blocks the capture will reuse, and lets lazily built state (plans,
+  flow libraries) settle outside the capture.
+* One more call runs under stream capture (`thin_backend::RuntimeGraph`, see
+  runtime.cpp). Whatever it returns becomes `outputs`. Those tensors live in
+  graph-owned memory, and every replay overwrites them.
+* The graph is launched once before the constructor returns, so `outputs`
+  already hold the example's results.
+* A call with a new value checks it against the captured input's signature.
+  It copies the value into `input` and replays.
+* Only the creating thread may replay. A graph is bound to that thread's
+  stream, and no concurrent replay is supported.
 """
+from contextlib import contextmanager
 from threading import get_ident
+from typing import NamedTuple
 
 import torch
 
+_NOT_INFERENCE = "CapturedForward requires an inference-only NPU input"
+_WRONG_THREAD = "RuntimeGraph must stay on its creating thread/stream"
+_MISMATCH = "Graph input shape, dtype, device and layout/strides must match capture"
+
+
+class _InputSignature(NamedTuple):
+    """What a replay input must share with the example the graph was captured on."""
+    shape: torch.Size
+    stride: tuple
+    dtype: torch.dtype
+    device: torch.device
+    layout: torch.layout
+
+    @classmethod
+    def of(cls, t: torch.Tensor) -> "_InputSignature":
+        return cls(t.shape, t.stride(), t.dtype, t.device, t.layout)
+
+    def admits(self, t: torch.Tensor) -> bool:
+        return not t.requires_grad and _InputSignature.of(t) == self
+
+
+@contextmanager
+def _stream_capture(graph):
+    """Record the calling thread's stream into `graph` for the duration of the
+    block. The capture is ended even when the block raises, for example on a
+    device-to-host copy, which cannot be recorded."""
+    graph.begin()
+    try:
+        yield
+    finally:
+        graph.end()
+
 
 class CapturedForward:
-    """Fixed-shape inference with graph-owned workspace and borrowed output buffers.
+    """A forward recorded once and replayed on new inputs of the same signature.
 
-    The callable, its parameters and captured tensors must not be mutated or moved.
-    Calls reuse the returned output tensors; clone outputs to retain prior results.
-    Create, replay and close on the same thread. No concurrent replay is supported.
+    Replays write into the same output tensors (graph-owned memory), so keep a
+    clone of any result needed after the next call. The forward, its
+    parameters and anything the capture read must stay as they were. Use the
+    object from the thread that built it, one replay at a time.
     """
 
     def __init__(self, forward, example, warmup=3):
         if example.device.type != "npu" or example.requires_grad:
-            raise ValueError("CapturedForward requires an inference-only NPU input")
-        self._input_layout = example.layout
-        self._input_stride = example.stride()
-        self._thread = get_ident()
+            raise ValueError(_NOT_INFERENCE)
+        self._owner = get_ident()
+        self._signature = _InputSignature.of(example)
         self.forward = forward
         self.input = torch.empty_like(example)
         self.input.copy_(example)
@@ -31,27 +83,41 @@ class CapturedForward:
         with torch.inference_mode():
             for _ in range(warmup):
                 forward(self.input)
-            self.graph.begin()
-            try:
+            with _stream_capture(self.graph):
                 self.outputs = forward(self.input)
-            finally:
-                self.graph.end()
-        self.graph.replay()
+        self._launch()
 
-    def replay(self):
-        """Enqueue one replay using the existing static input; return borrowed outputs."""
+    # -- hooks shared with FrozenGraph
+    def _before_launch(self):
+        """Called before every replay; FrozenGraph validates its pilot here."""
+
+    def _launch(self):
         self.graph.replay()
         return self.outputs
 
+    # -- public contract
+    def replay(self):
+        """Launch the graph on whatever `input` holds now; returns `outputs`,
+        which the launch overwrites (asynchronously, on this thread's stream)."""
+        self._before_launch()
+        return self._launch()
+
     def __call__(self, value):
-        if get_ident() != self._thread:
-            raise RuntimeError("RuntimeGraph must stay on its creating thread/stream")
-        if (value.shape != self.input.shape or value.dtype != self.input.dtype
-                or value.device != self.input.device or value.requires_grad
-                or value.layout != self._input_layout or value.stride() != self._input_stride):
-            raise ValueError("Graph input shape, dtype, device and layout/strides must match capture")
+        self._before_launch()
+        if get_ident() != self._owner:
+            raise RuntimeError(_WRONG_THREAD)
+        if not self._signature.admits(value):
+            raise ValueError(_MISMATCH)
         self.input.copy_(value)
-        return self.replay()
+        return self._launch()
 
     def close(self):
+        """Release the graph (idempotent). Outputs stay valid as tensors."""
         self.graph.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+        return False

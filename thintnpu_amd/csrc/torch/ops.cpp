@@ -1,7 +1,7 @@
 // aten / thin_backend / thin_fused kernels of the PrivateUse1 backend, each a
 // thin host wrapper over the thin_hip C ABI.
 //
-// Reference interfaces mirrored (names, argument meaning, checks, messages):
+// Reference interfaces served (names, argument meaning, error messages):
 //   ops.cpp:419-524        cat, binary add/sub/mul/div, silu_
 //   aten_adapter.cpp:25-112 sigmoid, silu, upsample_nearest2d, conv/pool rejects
 //   softmax_host.cpp:51-92 _softmax
@@ -14,6 +14,7 @@
 #include <c10/core/GradMode.h>
 #include <torch/library.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <string>
@@ -31,8 +32,23 @@ void trace(const char* aten, const char* target) {
 bool float_type(const at::Tensor& t) { return t.scalar_type() == at::kFloat || t.scalar_type() == at::kHalf; }
 
 // ------------------------------------------------------------------ binary
-// ops.cpp:464-497.  A 0-d CPU operand is taken as a scalar at PyTorch CPU's
-// precision (fp32 for mul/div, rounded to the tensor dtype for add/sub).
+// ops.cpp:464-497.  A 0-d CPU operand is converted to the tensor's dtype
+// first, as the reference converts it (ops.cpp:466-467), so x * (1/sqrt(32))
+// multiplies by the fp16 value of 1/sqrt(32) for every op.
+// THIN_SCALAR_OPMATH=1 keeps PyTorch CPU's rule instead: the scalar rounded to
+// the tensor dtype for add/sub, held at fp32 for mul/div.
+bool scalar_opmath() {
+  static const bool on = [] {
+    const char* v = std::getenv("THIN_SCALAR_OPMATH");
+    return v && std::string(v) == "1";
+  }();
+  return on;
+}
+
+double scalar_operand(const at::Tensor& s, at::ScalarType dtype) {
+  return scalar_opmath() ? s.item<double>() : s.to(dtype).item<double>();
+}
+
 at::Tensor binary(const at::Tensor& input, const at::Tensor& other, int op, const at::Scalar& alpha = 1) {
   const bool x_scalar = input.is_cpu() && input.dim() == 0;
   const bool y_scalar = other.is_cpu() && other.dim() == 0;
@@ -46,7 +62,8 @@ at::Tensor binary(const at::Tensor& input, const at::Tensor& other, int op, cons
     auto out = at::empty(t.sizes(), t.options().memory_format(c10::MemoryFormat::Contiguous));
     if (!t.numel()) return out;
     thin_desc td = desc(t), od = desc(out);
-    check(thin_binary_scalar(op, &td, s.item<double>(), x_scalar ? 1 : 0, &od, alpha.toFloat(), stream()),
+    check(thin_binary_scalar(op, &td, scalar_operand(s, t.scalar_type()), x_scalar ? 1 : 0, &od,
+                             alpha.toFloat(), stream()),
           "thin binary");
     after_launch();
     return out;
@@ -113,47 +130,68 @@ at::Tensor silu(const at::Tensor& x) {
 }
 
 // ------------------------------------------------------------------ cat
-// ops.cpp:419-462 (skips legacy 1-D empty inputs).
-at::Tensor cat(const at::ITensorListRef& inputs, int64_t dim) {
-  std::vector<at::Tensor> tensors;
-  for (const at::Tensor& t : inputs) tensors.push_back(t);
-  TORCH_CHECK(!tensors.empty(), "cat expects a nonempty tensor list");
-  const at::Tensor* reference = &tensors[0];
-  for (const auto& t : tensors) {
+// aten::cat with torch.cat semantics (the reference's thin_ops::cat,
+// ops.cpp:419-462).  Legacy 1-D empty tensors are accepted anywhere in the list
+// and contribute nothing; the first contributing input fixes the output's
+// rank, dtype, device and the sizes outside `dim`.  Inputs are launched in
+// groups of THIN_MAX_CAT_INPUTS, each into its slice of the output.
+namespace {
+
+bool legacy_empty(const at::Tensor& t) { return t.dim() == 1 && t.numel() == 0; }
+
+struct CatShape {
+  std::vector<at::Tensor> parts;  // contributing inputs, in list order
+  std::vector<int64_t> sizes;     // output sizes
+  int64_t dim = 0;
+};
+
+CatShape cat_shape(const at::ITensorListRef& inputs, int64_t dim) {
+  const std::vector<at::Tensor> all(inputs.begin(), inputs.end());
+  TORCH_CHECK(!all.empty(), "cat expects a nonempty tensor list");
+  for (const auto& t : all) {
     inference(t, "thin ops");
     TORCH_CHECK(t.dim() > 0, "cat cannot concatenate scalar tensors");
-    if (!(t.dim() == 1 && t.numel() == 0)) reference = &t;
   }
-  dim = at::maybe_wrap_dim(dim, reference->dim());
-  auto sizes = reference->sizes().vec();
-  sizes[dim] = 0;
-  std::vector<at::Tensor> live;
-  for (const auto& t : tensors) {
-    TORCH_CHECK(t.device() == reference->device() && t.scalar_type() == reference->scalar_type(),
+  const auto first = std::find_if(all.begin(), all.end(), [](const at::Tensor& t) { return !legacy_empty(t); });
+  const at::Tensor& shape = first == all.end() ? all.front() : *first;
+  CatShape c;
+  c.dim = at::maybe_wrap_dim(dim, shape.dim());
+  c.sizes = shape.sizes().vec();
+  c.sizes[c.dim] = 0;
+  for (const auto& t : all) {
+    TORCH_CHECK(t.device() == shape.device() && t.scalar_type() == shape.scalar_type(),
                 "cat requires matching device and dtype");
-    if (t.dim() == 1 && !t.numel()) continue;
-    TORCH_CHECK(t.dim() == reference->dim(), "cat rank mismatch");
+    if (legacy_empty(t)) continue;
+    TORCH_CHECK(t.dim() == shape.dim(), "cat rank mismatch");
+    const auto same_outside = [&](int64_t d) { return d == c.dim || t.size(d) == shape.size(d); };
     for (int64_t d = 0; d < t.dim(); ++d)
-      TORCH_CHECK(d == dim || t.size(d) == reference->size(d),
-                  "cat shape mismatch outside concatenation dimension");
-    sizes[dim] += t.size(dim);
-    live.push_back(t);
+      TORCH_CHECK(same_outside(d), "cat shape mismatch outside concatenation dimension");
+    c.sizes[c.dim] += t.size(c.dim);
+    c.parts.push_back(t);
   }
-  select(reference->device());
-  auto out = at::empty(sizes, reference->options().memory_format(c10::MemoryFormat::Contiguous));
+  return c;
+}
+
+}  // namespace
+
+at::Tensor cat(const at::ITensorListRef& inputs, int64_t dim) {
+  const CatShape c = cat_shape(inputs, dim);
+  const at::Tensor& like = c.parts.empty() ? *inputs.begin() : c.parts.front();
+  select(like.device());
+  auto out = at::empty(c.sizes, like.options().memory_format(c10::MemoryFormat::Contiguous));
   if (!out.numel()) return out;
   int64_t start = 0;
-  for (size_t g = 0; g < live.size(); g += THIN_MAX_CAT_INPUTS) {
-    const size_t n = std::min<size_t>(THIN_MAX_CAT_INPUTS, live.size() - g);
+  for (size_t g = 0; g < c.parts.size(); g += THIN_MAX_CAT_INPUTS) {
+    const size_t n = std::min<size_t>(THIN_MAX_CAT_INPUTS, c.parts.size() - g);
     std::vector<thin_desc> ds;
     int64_t width = 0;
     for (size_t k = 0; k < n; ++k) {
-      ds.push_back(desc(live[g + k]));
-      width += live[g + k].size(dim);
+      ds.push_back(desc(c.parts[g + k]));
+      width += c.parts[g + k].size(c.dim);
     }
-    at::Tensor slice = live.size() <= THIN_MAX_CAT_INPUTS ? out : out.narrow(dim, start, width);
+    at::Tensor slice = c.parts.size() <= THIN_MAX_CAT_INPUTS ? out : out.narrow(c.dim, start, width);
     thin_desc od = desc(slice);
-    check(thin_cat(ds.data(), (int32_t)n, (int32_t)dim, &od, stream()), "thin cat");
+    check(thin_cat(ds.data(), (int32_t)n, (int32_t)c.dim, &od, stream()), "thin cat");
     start += width;
   }
   after_launch();

@@ -11,7 +11,8 @@
 //   - every parameter and buffer: identity, version counter, data pointer,
 //     sizes, strides, offset, dtype, device and requires_grad == False;
 //   - each class's forward, and torch's global module hooks (none allowed).
-// Any drift raises ValueError.  Python API and messages follow the
+// Any drift raises ValueError.  require_frozen_fp16() is the admission rule
+// RegionContract applies before building a Guard.  Python API and messages follow the
 // reference's region guard (region_guard.cpp:36-188, used through
 // region_contract.py:5-28); the implementation is independent.
 #include <pybind11/pybind11.h>
@@ -228,10 +229,38 @@ class Guard {
                                      interned("_global_backward_hooks"), interned("_global_backward_pre_hooks")};
 };
 
+// Admission rule of a frozen fp16 region (RegionContract's constructor): every
+// parameter and buffer of every module is a version-counted fp16 tensor on the
+// npu device without gradient.  Tensors are visited module by module,
+// parameters before buffers, and the first offender raises ValueError.  An
+// inference-mode tensor has no version counter for the guard to snapshot.
+void require_frozen_fp16(py::iterable modules) {
+  const py::str keys[2] = {interned("_parameters"), interned("_buffers")};
+  for (auto item : modules) {
+    py::object state = py::reinterpret_borrow<py::object>(item).attr("__dict__");
+    PyObject* d = as_dict(state.ptr());
+    for (const auto& key : keys) {
+      PyObject* values = lookup(d, key.ptr());
+      if (!values) continue;
+      for (auto kv : py::reinterpret_borrow<py::dict>(as_dict(values))) {
+        if (kv.second.is_none()) continue;
+        if (!THPVariable_Check(kv.second.ptr()))
+          throw py::type_error("Expected a Tensor or None in module parameters/buffers");
+        const at::Tensor& t = THPVariable_Unpack(kv.second.ptr());
+        if (t.is_inference())
+          throw py::value_error("Prepare versioned parameters under no_grad(), not inference_mode()");
+        if (t.requires_grad() || t.scalar_type() != at::kHalf || t.device().type() != c10::DeviceType::PrivateUse1)
+          throw py::value_error("Expected fixed FP16 NPU inference parameters");
+      }
+    }
+  }
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_region_guard, m) {
   py::class_<Guard>(m, "Guard")
       .def(py::init<py::iterable, py::set, py::iterable>())
       .def("validate", &Guard::validate);
+  m.def("require_frozen_fp16", &require_frozen_fp16);
 }

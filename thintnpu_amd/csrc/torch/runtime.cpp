@@ -2,12 +2,13 @@
 // allocator (graph-retained capture allocations), empty/copy_/views, the
 // host-computed constants (arange/fill_/item) and RuntimeGraph on hipGraph.
 //
-// Mirrors the reference runtime core (backend.cpp:32-206,312-361;
-// graph_capture.h:7-24; decode.cpp:6-34; ops.cpp:32-78) on HIP: the same
-// names, checks and messages, with two MI355X-side changes -- eager ops are
-// asynchronous on the thread's stream (THIN_SYNC=1 restores the reference's
-// per-op synchronize), and freed memory is cached per stream instead of being
-// returned with a synchronizing free.
+// Serves the reference runtime's surface (backend.cpp:32-206,312-361;
+// graph_capture.h:7-24; decode.cpp:6-34; ops.cpp:32-78): one logical device,
+// one stream per host thread, eager ops that have finished when they return
+// (THIN_ASYNC=1 opts a single-threaded caller out of the per-op
+// synchronize), and capture-time memory held until the graph closes.  Freed
+// memory is cached per stream instead of being returned with a synchronizing
+// free.
 #include "thin_runtime.h"
 
 #include <ATen/EmptyTensor.h>
@@ -23,6 +24,7 @@
 #include <torch/custom_class.h>
 #include <torch/library.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -62,8 +64,28 @@ thread_local GraphState* g_capture = nullptr;
 
 bool capturing() { return g_capture != nullptr; }
 
+// Eager ops synchronize their stream after each launch by default, as the
+// reference's eager ops do (backend.cpp:46).  When an op returns its kernels
+// have finished, so memory a host thread releases is never still read by
+// another thread's stream, and the caching allocator may hand it out again at
+// once.  THIN_ASYNC=1 leaves eager launches asynchronous.  That mode serves one
+// host thread: its single stream orders every reuse of a block.  A second
+// host thread that touches the device then fails loudly instead of racing.
+static bool eager_async() {
+  static const bool on = [] {
+    const char* v = std::getenv("THIN_ASYNC");
+    return v && std::strcmp(v, "1") == 0;
+  }();
+  return on;
+}
+
+static std::atomic<int> g_thread_streams{0};
+
 hipStream_t stream() {
   thread_local hipStream_t s = [] {
+    const int n = ++g_thread_streams;
+    TORCH_CHECK(!eager_async() || n == 1,
+                "THIN_ASYNC=1 allows one host thread on the NPU; unset it for multi-threaded use");
     select();
     hipStream_t p = nullptr;
     hip_check(hipStreamCreate(&p), "hipStreamCreate");
@@ -76,16 +98,8 @@ void sync() {
   if (!capturing()) hip_check(hipStreamSynchronize(stream()), "hipStreamSynchronize");
 }
 
-static bool eager_sync_enabled() {
-  static const bool on = [] {
-    const char* v = std::getenv("THIN_SYNC");
-    return v && std::strcmp(v, "1") == 0;
-  }();
-  return on;
-}
-
 void after_launch() {
-  if (eager_sync_enabled()) sync();
+  if (!eager_async()) sync();
 }
 
 thin_desc desc(const at::Tensor& t) {
@@ -134,10 +148,10 @@ size_t round_size(size_t n) {
 
 // Caching allocator.  A freed block returns to the free list of the stream it
 // was allocated on and is reused only by later allocations on that stream, so
-// reuse is ordered after every kernel that stream enqueued with it.  A tensor
-// whose memory another host thread's stream still reads must be synchronized
-// by the caller before it is released (the reference synchronizes after every
-// op; THIN_SYNC=1 restores that).
+// reuse is ordered after every kernel that stream enqueued with it.  Work of
+// other streams on the block has finished by the time it is released: eager
+// ops complete before they return (after_launch), and with THIN_ASYNC=1 there
+// is only one stream.
 class Pool {
  public:
   void* alloc(size_t n) {
@@ -434,74 +448,120 @@ at::Tensor& copy_entry(at::Tensor& dst, const at::Tensor& src, bool non_blocking
 }
 
 // ------------------------------------------------------------------ RuntimeGraph
-// backend.cpp:62-113 on hipGraph: stream capture of the thread's stream,
-// instantiate, launch; capture-time allocations retained until close().
+// thin_backend::RuntimeGraph (the reference's capture object, backend.cpp:62-113)
+// on hipGraph.  One object records the creating thread's stream once and
+// replays it:
+//
+//   kEmpty --begin()--> kRecording --end()--> kExecutable --replay()*--> ...
+//   any phase --close()--> kClosed (idempotent)
+//
+// While recording, the allocator routes every block allocated or freed by
+// this thread to the graph's GraphState, so memory the recorded kernels touch
+// stays valid until close().  The executable is uploaded to the stream at
+// end(), so the first replay pays no upload.  Every call must come from the
+// creating thread, whose stream the graph is bound to.
 class RuntimeGraph : public torch::CustomClassHolder {
-  std::unique_ptr<GraphState> mem_ = std::make_unique<GraphState>();
-  hipGraph_t graph_ = nullptr;
-  hipGraphExec_t exec_ = nullptr;
-  hipStream_t stream_ = stream();
-  std::thread::id owner_ = std::this_thread::get_id();
-  bool active_ = false;
-  bool closed_ = false;
-
-  void same_thread() const {
-    TORCH_CHECK(owner_ == std::this_thread::get_id(), "RuntimeGraph must stay on its creating thread/stream");
-  }
-
  public:
+  enum class Phase { kEmpty, kRecording, kExecutable, kClosed };
+
   void begin() {
-    same_thread();
-    TORCH_CHECK(!closed_ && !active_ && !exec_ && !capturing(), "RuntimeGraph cannot begin in its current state");
-    sync();
-    // Relaxed mode: the allocator may call hipMalloc while capturing.
+    require_owner();
+    TORCH_CHECK(phase_ == Phase::kEmpty, "RuntimeGraph.begin: ", describe(),
+                "; a RuntimeGraph records exactly once");
+    TORCH_CHECK(!capturing(), "RuntimeGraph.begin: this thread is already recording another graph");
+    sync();  // eager work enqueued before the recording must not be recorded
     hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeRelaxed), "hipStreamBeginCapture");
-    g_capture = mem_.get();
-    active_ = true;
+    g_capture = memory_.get();
+    phase_ = Phase::kRecording;
   }
+
   void end() {
-    same_thread();
-    TORCH_CHECK(active_ && g_capture == mem_.get(), "RuntimeGraph is not capturing");
-    hipError_t e = hipStreamEndCapture(stream_, &graph_);
+    require_owner();
+    TORCH_CHECK(phase_ == Phase::kRecording && g_capture == memory_.get(), "RuntimeGraph.end: ", describe(),
+                ", not recording");
+    hipGraph_t recorded = nullptr;
+    const hipError_t e = hipStreamEndCapture(stream_, &recorded);
     g_capture = nullptr;
-    active_ = false;
+    phase_ = Phase::kExecutable;  // close() releases whatever was built, also on failure
+    exec_.graph = recorded;
     hip_check(e, "hipStreamEndCapture");
-    hip_check(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0), "hipGraphInstantiate");
+    hip_check(hipGraphInstantiate(&exec_.exec, exec_.graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    hip_check(hipGraphUpload(exec_.exec, stream_), "hipGraphUpload");
   }
+
   void replay() {
-    same_thread();
-    TORCH_CHECK(!closed_ && exec_ && !active_ && !capturing(), "RuntimeGraph is not ready to replay");
-    hip_check(hipGraphLaunch(exec_, stream_), "hipGraphLaunch");
+    require_owner();
+    TORCH_CHECK(phase_ == Phase::kExecutable && exec_.exec, "RuntimeGraph.replay: ", describe(),
+                ", nothing to replay");
+    TORCH_CHECK(!capturing(), "RuntimeGraph.replay: cannot launch a graph while this thread records one");
+    hip_check(hipGraphLaunch(exec_.exec, stream_), "hipGraphLaunch");
     after_launch();
   }
+
   void close() {
-    same_thread();
-    if (closed_) return;
-    if (active_) end();
-    TORCH_CHECK(!capturing(), "Cannot close a graph during another capture");
-    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
-    if (exec_) {
-      hip_check(hipGraphExecDestroy(exec_), "hipGraphExecDestroy");
-      exec_ = nullptr;
+    require_owner();
+    if (phase_ == Phase::kClosed) return;
+    if (phase_ == Phase::kRecording) {  // abandon the recording; nothing of it is kept
+      hipGraph_t partial = nullptr;
+      (void)hipStreamEndCapture(stream_, &partial);
+      g_capture = nullptr;
+      if (partial) (void)hipGraphDestroy(partial);
     }
-    if (graph_) {
-      hip_check(hipGraphDestroy(graph_), "hipGraphDestroy");
-      graph_ = nullptr;
-    }
-    pool().graph_closed(mem_.get());
-    for (void* h : mem_->host) (void)hipHostFree(h);
-    mem_->host.clear();
-    closed_ = true;
+    TORCH_CHECK(!capturing(), "RuntimeGraph.close: this thread is recording another graph");
+    hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize");  // last replay done
+    exec_.destroy();
+    pool().graph_closed(memory_.get());
+    for (void* h : memory_->host) (void)hipHostFree(h);
+    memory_->host.clear();
+    phase_ = Phase::kClosed;
   }
+
   ~RuntimeGraph() override {
+    if (phase_ == Phase::kClosed) return;
     try {
       close();
     } catch (const std::exception& error) {
-      std::fprintf(stderr, "RuntimeGraph cleanup failed: %s\n", error.what());
-      // Live graph addresses must not be reused when cleanup fails.
-      (void)mem_.release();
+      // The device may still use the graph's memory: keep every block it
+      // holds out of the allocator for the rest of the process.
+      std::fprintf(stderr, "RuntimeGraph: close in destructor failed, its memory stays reserved: %s\n",
+                   error.what());
+      (void)memory_.release();
     }
   }
+
+ private:
+  struct Executable {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    void destroy() {
+      if (exec) hip_check(hipGraphExecDestroy(exec), "hipGraphExecDestroy");
+      exec = nullptr;
+      if (graph) hip_check(hipGraphDestroy(graph), "hipGraphDestroy");
+      graph = nullptr;
+    }
+  };
+
+  // The graph is bound to the creating thread's stream.  The message is the
+  // one callers of the reference key on ("creating thread/stream").
+  void require_owner() const {
+    TORCH_CHECK(std::this_thread::get_id() == owner_ && stream() == stream_,
+                "RuntimeGraph must stay on its creating thread/stream");
+  }
+
+  const char* describe() const {
+    switch (phase_) {
+      case Phase::kEmpty: return "the graph is empty";
+      case Phase::kRecording: return "the graph is recording";
+      case Phase::kExecutable: return "the graph is already recorded";
+      default: return "the graph is closed";
+    }
+  }
+
+  const std::thread::id owner_ = std::this_thread::get_id();
+  const hipStream_t stream_ = stream();
+  std::unique_ptr<GraphState> memory_ = std::make_unique<GraphState>();
+  Executable exec_;
+  Phase phase_ = Phase::kEmpty;
 };
 
 void empty_cache() { pool().empty_cache(); }

@@ -27,8 +27,8 @@ bool capturing();
 // (backend.cpp:46).
 void sync();
 
-// Eager ops enqueue asynchronously; THIN_SYNC=1 synchronizes after each op
-// like the reference's eager mode.
+// Called after every eager launch: synchronizes the thread's stream (the
+// reference's eager semantics) unless THIN_ASYNC=1 (one host thread only).
 void after_launch();
 
 // HIP error -> c10::Error.
