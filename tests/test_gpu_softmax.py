@@ -236,3 +236,24 @@ def test_softmax_short_columns(gpu):
     view = logits.view(2, 4, 16, a).transpose(1, 2)
     got = capi.softmax(logits.to(gpu).view(2, 4, 16, a).transpose(1, 2), 1).cpu()
     check_softmax(got, view, 1, what="DFL bin view")
+
+
+@pytest.mark.parametrize("half_to_float", [False, True])
+def test_dfl_softmax_eight_and_two_column_forms_agree(gpu, half_to_float):
+    """The DFL bin view runs eight columns per thread when every row is
+    16-byte aligned and two when only 4-byte aligned; both evaluate the same
+    expressions in the same order, so their outputs are bit-identical."""
+    from oracle.numerics import bits_equal
+    from thintnpu_amd import capi
+    a = 8400
+    logits = normal16((2, 64, a + 2), 19, std=3.0)
+    logits[0, 17, 9] = float("nan")
+    logits[1, 32:48, 100] = float("-inf")
+    logits[1, 5, 200] = float("inf")
+    d = logits.to(gpu)
+    two = capi.softmax(d[..., 2:].view(2, 4, 16, a).transpose(1, 2), 1, half_to_float).cpu()  # 4-byte aligned rows
+    eight = capi.softmax(d[..., 2:].contiguous().view(2, 4, 16, a).transpose(1, 2), 1, half_to_float).cpu()
+    nan = torch.isnan(two)
+    assert torch.equal(torch.isnan(eight), nan)  # NaN payloads may differ between the forms
+    assert bits_equal(eight[~nan], two[~nan])
+    check_softmax(eight, logits[..., 2:].reshape(2, 4, 16, a).transpose(1, 2), 1, half_to_float, what="eight-column")

@@ -12,6 +12,8 @@
 
 #include <string.h>
 
+#include <algorithm>
+
 namespace thin {
 namespace {
 
@@ -27,6 +29,15 @@ template <bool FAST>
 __device__ __forceinline__ float expo(float x) {
   if (FAST) return fast_exp(x);
   return expf(x);
+}
+
+// exp(x - m) of the column kernels.  FAST (fp16 output): exp2(x*log2e -
+// m*log2e) as one fma, the row kernel's form; otherwise expf(x - m).
+template <bool FAST>
+__device__ __forceinline__ float expd(float x, float m) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  if (FAST) return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -(m * kLog2e)));
+  return expf(x - m);
 }
 
 template <typename T> __device__ __forceinline__ float ldf(const T* p) { return (float)*p; }
@@ -219,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
       for (int r = 0; r < RREG; ++r) {
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-          e[r][j] = r < (int)p.R ? expo<FAST>((float)reg[r].e[j] - m[j]) : 0.f;
+          e[r][j] = r < (int)p.R ? expd<FAST>((float)reg[r].e[j], m[j]) : 0.f;
           s[j] += e[r][j];
         }
       }
@@ -241,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
     for (int r = 0; r < RREG; ++r) {
       if (r < (int)p.R) {
 #pragma unroll
-        for (int j = 0; j < V; ++j) s[j] += expo<FAST>((float)reg[r].e[j] - m[j]);
+        for (int j = 0; j < V; ++j) s[j] += expd<FAST>((float)reg[r].e[j], m[j]);
       }
     }
 #pragma unroll
@@ -249,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
       if (r < (int)p.R) {
         WO w;
 #pragma unroll
-        for (int j = 0; j < V; ++j) w.e[j] = (TO)(expo<FAST>((float)reg[r].e[j] - m[j]) / s[j]);
+        for (int j = 0; j < V; ++j) w.e[j] = (TO)(expd<FAST>((float)reg[r].e[j], m[j]) / s[j]);
         *reinterpret_cast<WO*>(oc + r * p.orr) = w;
       }
     }
@@ -263,14 +274,154 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
   for (uint32_t r = 0; r < p.R; ++r) {
     WI w = *reinterpret_cast<const WI*>(xc + r * p.xr);
 #pragma unroll
-    for (int j = 0; j < V; ++j) s[j] += expo<FAST>((float)w.e[j] - m[j]);
+    for (int j = 0; j < V; ++j) s[j] += expd<FAST>((float)w.e[j], m[j]);
   }
   for (uint32_t r = 0; r < p.R; ++r) {
     WI w = *reinterpret_cast<const WI*>(xc + r * p.xr);
     WO o;
 #pragma unroll
-    for (int j = 0; j < V; ++j) o.e[j] = (TO)(expo<FAST>((float)w.e[j] - m[j]) / s[j]);
+    for (int j = 0; j < V; ++j) o.e[j] = (TO)(expd<FAST>((float)w.e[j], m[j]) / s[j]);
     *reinterpret_cast<WO*>(oc + r * p.orr) = o;
+  }
+}
+
+// Short fp16 column reductions (R <= 16 rows) over 16-byte column groups: the
+// DFL bin softmax over the [B,16,4,A] view (R = 16 rows at stride A).  A unit
+// is eight adjacent columns; SPLIT lanes share a unit, each holding 16/SPLIT
+// of its rows as one 16-byte load per row, so a load instruction moves
+// 64/SPLIT units (1 KB / SPLIT) of SPLIT rows.  The column max travels between
+// the lanes of a unit by xor shuffles.  The sum is taken in row order: part q
+// adds its rows to the running sum it receives from part q-1, and the total
+// is broadcast back.  That is the column kernel's arithmetic term for term
+// (e = exp(x - max), sums in row order, e * (1/s) for fp16 output, expf and
+// e / s for fp32 output), so both kernels give the same bits.  The column max
+// only stabilises the exponentials: a packed fp16 maximum that skips NaN
+// still leaves a NaN column all NaN (its e and so its sum are NaN), as on CPU.
+//
+// LOOP: each wave walks its units with a grid stride and loads its next units
+// before it computes and stores the current ones, so HBM reads, the
+// exponentials and the stores of different rounds overlap instead of every
+// wave of a single-round launch loading, computing and storing in lockstep.
+// Without LOOP the grid covers every unit once (small launches).
+template <typename TO, bool FAST, bool NT, int SPLIT, bool LOOP, bool R16>
+__global__ __launch_bounds__(kThreads) void softmax_cols8_kernel(SoftmaxPlan p) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int RP = 16 / SPLIT;            // rows per lane
+  constexpr uint32_t kSlots = 64 / SPLIT;   // units per wave and round
+  const uint32_t lane = threadIdx.x & 63u, part = lane / kSlots, slot = lane % kSlots;
+  const uint32_t row0 = part * RP;
+  const uint32_t R = R16 ? 16u : p.R;  // R16: every row of every lane is live (no masks)
+  const uint32_t stride = gridDim.x * kWaves * kSlots;
+  // Blocks are dealt to the 8 XCDs round robin; block b runs as logical block
+  // (b % 8) * (grid / 8) + b / 8, so each XCD walks one contiguous run of
+  // units and the 128-byte lines that neighbouring units share in a row stay
+  // in one L2.  The grid is a multiple of 8.
+  const uint32_t logical = (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  uint32_t base = (logical * kWaves + (threadIdx.x >> 6)) * kSlots;  // wave-uniform
+  if (base >= p.units) return;
+
+  auto load = [&](uint32_t u, h8 (&v)[RP]) {
+    if (u < p.units) {
+      int64_t xo, oo;
+      col_offsets(p, u * 8u, xo, oo);
+      const _Float16* xc = static_cast<const _Float16*>(p.x) + xo;
+#pragma unroll
+      for (int i = 0; i < RP; ++i) {
+        // rows past R re-read row R - 1 (every load stays unconditional) and are masked below
+        const u4* src = reinterpret_cast<const u4*>(xc + (int64_t)(R16 ? row0 + i : min(row0 + i, R - 1)) * p.xr);
+        v[i] = __builtin_bit_cast(h8, NT ? __builtin_nontemporal_load(src) : *src);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < RP; ++i) v[i] = (h8)(_Float16)0;
+    }
+  };
+
+  h8 cur[RP], nxt[RP];
+  load(base + slot, cur);
+  for (;;) {
+    const uint32_t next = base + stride;
+    if (LOOP && next < p.units) load(next + slot, nxt);
+    const uint32_t u = base + slot;
+    // column max over this lane's rows, then across the unit's lanes
+    h8 mh = (h8)(_Float16)(-__builtin_inff());
+#pragma unroll
+    for (int i = 0; i < RP; ++i)
+      if (R16 || row0 + i < R) mh = __builtin_elementwise_max(mh, cur[i]);
+#pragma unroll
+    for (uint32_t o = kSlots; o < 64; o <<= 1) {
+      u4 w = __builtin_bit_cast(u4, mh), t;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) t[q] = (uint32_t)__shfl_xor((int)w[q], (int)o, 64);
+      mh = __builtin_elementwise_max(mh, __builtin_bit_cast(h8, t));
+    }
+    float m[8], e[RP][8], s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      m[j] = (float)mh[j];
+      s[j] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < RP; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[i][j] = R16 || row0 + i < R ? expd<FAST>((float)cur[i][j], m[j]) : 0.f;
+    // running sum in row order: part q continues the sum of part q - 1
+#pragma unroll
+    for (uint32_t q = 0; q < (uint32_t)SPLIT; ++q) {
+      if (part == q) {
+#pragma unroll
+        for (int i = 0; i < RP; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) s[j] += e[i][j];
+      }
+      const uint32_t from = slot + (q + 1 < (uint32_t)SPLIT ? q : (uint32_t)SPLIT - 1) * kSlots;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float t = __shfl(s[j], (int)from, 64);
+        if (part == q + 1 || q + 1 == (uint32_t)SPLIT) s[j] = t;
+      }
+    }
+    float inv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) inv[j] = 1.0f / s[j];
+    if (u < p.units) {
+      int64_t xo, oo;
+      col_offsets(p, u * 8u, xo, oo);
+      TO* oc = static_cast<TO*>(p.out) + oo;
+#pragma unroll
+      for (int i = 0; i < RP; ++i) {
+        if (R16 || row0 + i < R) {
+          u4* dst = reinterpret_cast<u4*>(oc + (int64_t)(row0 + i) * p.orr);
+          u4 w[sizeof(TO) / 2];
+          if constexpr (sizeof(TO) == 2) {
+            h8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = (_Float16)(FAST ? e[i][j] * inv[j] : e[i][j] / s[j]);
+            w[0] = __builtin_bit_cast(u4, o);
+          } else {
+            f4 lo, hi;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              lo[j] = FAST ? e[i][j] * inv[j] : e[i][j] / s[j];
+              hi[j] = FAST ? e[i][4 + j] * inv[4 + j] : e[i][4 + j] / s[4 + j];
+            }
+            w[0] = __builtin_bit_cast(u4, lo);
+            w[1] = __builtin_bit_cast(u4, hi);
+          }
+#pragma unroll
+          for (int q = 0; q < (int)(sizeof(TO) / 2); ++q) {
+            if constexpr (NT) __builtin_nontemporal_store(w[q], dst + q);
+            else dst[q] = w[q];
+          }
+        }
+      }
+    }
+    if (!LOOP || next >= p.units) break;
+#pragma unroll
+    for (int i = 0; i < RP; ++i) cur[i] = nxt[i];
+    base = next;
   }
 }
 
@@ -512,6 +663,35 @@ void launch_rows(const SoftmaxPlan& p, int64_t chunks, uint64_t rows, hipStream_
 #undef THIN_ROWG
 }
 
+// Units of eight columns per lane group.  Launches of at least 65536 units
+// (the DFL bin softmax at N=32: 134400) run two lanes per unit in a 512-block
+// grid-stride loop (8 waves per CU, about two rounds each); smaller ones run
+// four lanes per unit, one round, for more waves in flight.  Measured on the
+// [32,16,4,8400] view: 14.9 us (16.8 with the two-column kernel), which is the
+// time of a plain 16-byte copy with the same sixteen-rows-per-unit access
+// pattern (14.8 us); a linear copy of the same bytes takes 12.6 us.
+constexpr uint32_t kCols8Blocks = 512;
+
+template <typename TO, bool FAST>
+void launch_cols8(const SoftmaxPlan& p, bool nt, hipStream_t stream) {
+  const bool wide = p.units >= 32u * kCols8Blocks * kWaves;
+  const uint32_t per_block = (wide ? 32u : 16u) * kWaves;
+  const uint32_t grid = wide ? kCols8Blocks : ((p.units + per_block - 1) / per_block + 7u) / 8u * 8u;
+#define THIN_COLS8(NT, SPLIT, LOOP, R16) \
+  hipLaunchKernelGGL((softmax_cols8_kernel<TO, FAST, NT, SPLIT, LOOP, R16>), dim3(grid), dim3(kThreads), 0, stream, p)
+#define THIN_COLS8_R(NT, SPLIT, LOOP) \
+  if (p.R == 16) THIN_COLS8(NT, SPLIT, LOOP, true); else THIN_COLS8(NT, SPLIT, LOOP, false)
+  if (wide) {
+    if (nt) { THIN_COLS8_R(true, 2, true); }
+    else { THIN_COLS8_R(false, 2, true); }
+  } else {
+    if (nt) { THIN_COLS8_R(true, 4, false); }
+    else { THIN_COLS8_R(false, 4, false); }
+  }
+#undef THIN_COLS8_R
+#undef THIN_COLS8
+}
+
 template <typename TI, typename TO, bool FAST>
 thin_status launch_softmax(const thin_desc* x, int dim, const thin_desc* out, hipStream_t stream) {
   SoftmaxPlan p;
@@ -566,10 +746,19 @@ thin_status launch_softmax(const thin_desc* x, int dim, const thin_desc* out, hi
   // flight ([32,16,4,8400]: 16.8 us; 19.3 us with four columns per thread and
   // their exponentials kept, 37 us with eight; streaming loads and stores
   // measured the same 16.8 us)
+  // Eight fp16 columns per thread through 16-byte accesses when every row
+  // and column group is 16-byte aligned (the DFL view with A % 8 == 0).
+  bool oct = sizeof(TI) == 2 && R <= 16 && p.nd >= 1 && p.xs[0] == 1 && p.os[0] == 1 && p.size[0] % 8 == 0 &&
+             aligned(x->data, 16) && aligned(out->data, 16) && p.xr % 8 == 0 && p.orr % 8 == 0;
+  for (int i = 1; oct && i < p.nd; ++i) oct = p.xs[i] % 8 == 0 && p.os[i] % 8 == 0;
   bool pair = sizeof(TI) == 2 && R <= 16 && p.nd >= 1 && p.xs[0] == 1 && p.os[0] == 1 && p.size[0] % 2 == 0 &&
               aligned(x->data, 4) && aligned(out->data, 2 * sizeof(TO)) && p.xr % 2 == 0 && p.orr % 2 == 0;
   for (int i = 1; pair && i < p.nd; ++i) pair = p.xs[i] % 2 == 0 && p.os[i] % 2 == 0;
-  if (pair) {
+  if (oct) {
+    p.units = (uint32_t)(cols / 8);
+    const bool nt = (int64_t)cols * R * (int64_t)(sizeof(TI) + sizeof(TO)) >= kStreamingBytes;
+    launch_cols8<TO, FAST>(p, nt, stream);
+  } else if (pair) {
     p.units = (uint32_t)(cols / 2);
     const uint32_t grid = (p.units + kThreads - 1) / kThreads;
     hipLaunchKernelGGL((softmax_col_kernel<TI, TO, 2, 16, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
