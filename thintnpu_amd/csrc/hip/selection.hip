@@ -18,6 +18,7 @@
 
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 
 namespace thin {
@@ -694,19 +695,497 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackArgs p) {
   }
 }
 
+// ---------------------------------------------------------------- split selection
+// The selection spread over many workgroups, for one image or a few.  Records
+// are 32-bit (key << 16 | index): the stage-1 index is the anchor, the stage-2
+// index the flat pair index rank * nc + class; both fit 16 bits here, keys
+// never reach 0xffff (the largest is -inf's 0xfc00), so 0xffffffff pads.
+//
+//   slice  (grid lists x B): class max of kSlice anchors, then the slice's
+//          records sorted -> lists1[b][p], bits1 / cls1.
+//   merge1 (grid kMergeBlocks x B): the stage-1 top K of the sorted slices;
+//          writes stage1[b][rank] and the threshold key T1 (class-agnostic:
+//          packs the output rows instead).
+//   pairs  (grid pair blocks x B): block p takes stage-1 ranks [p*RB, ...),
+//          gathers their nc scores, keeps pairs keyed at most T1 (the K
+//          class-max pairs of the stage-1 anchors are among them, so the
+//          K-th best pair is keyed at most T1) and writes them sorted, at most
+//          K, to lists2[b][p].
+//   merge2 (grid kMergeBlocks x B): the top K of the pair lists; packs rows.
+//
+// Merging sorted lists.  With q such that the first min(q, n_p) records of
+// the lists number at least K, every record above R = max_p
+// list_p[min(q, n_p) - 1] has at least K records below it, so only records up
+// to R are candidates.  A candidate at position i of list p has rank i plus,
+// for every other list, the number of its candidates below it.  Each merge
+// block ranks a share of the candidates; the ranks are a permutation, so the
+// shares write disjoint rows.
+//
+// These kernels avoid long chains of dependent LDS accesses (about 130 cycles
+// each on gfx950): sorts are rank counts (every record compared with every
+// other, independent vector loads), and list counts are vector scans of the
+// short candidate prefixes.
+constexpr uint32_t kSlice = 256;         // anchors per stage-1 list
+constexpr uint32_t kMaxLists = 64;       // lists per batch and stage
+constexpr uint32_t kMergeBlocks = 16;    // merge workgroups per batch
+constexpr uint32_t kSplitMaxK = 1024;
+constexpr uint32_t kPairCap = 4096;      // gathered pairs per pairs block
+constexpr uint32_t kMerge2Words = 16384; // pair lists per batch: pair_blocks * K records
+constexpr uint32_t kPad = 0xffffffffu;
+// LDS pitch of a stage-1 list: 260 words puts list l's vectors on banks 4l
+// mod 64 (a 256-word pitch would put every list on the same banks, and the
+// lanes that scan different lists would serialise).
+constexpr uint32_t kSliceLds = kSlice + 4;
+
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+struct SplitPlan {
+  Layout L;
+  uint32_t A, nc, K;
+  uint32_t lists1;        // stage-1 lists per batch: ceil(A / kSlice)
+  uint32_t q1;            // stage-1 prefix length (host: depends on A and K only)
+  uint32_t pair_blocks;   // stage-2 lists per batch
+  uint32_t ranks_per;     // stage-1 ranks per pairs block
+  uint32_t pitch2;        // words per pair list: K rounded up to a multiple of 4
+  uint32_t lds_pitch2;    // the same list's LDS pitch, 4 mod 64 words (see kSliceLds)
+  int32_t agnostic;
+  int32_t vec_classes;    // anchors contiguous in aligned 16-byte groups (slice_kernel)
+  uint16_t* bits1;        // [B, A]
+  int32_t* cls1;          // [B, A]
+  uint32_t* lists1_rec;   // [B, lists1, kSlice]
+  int32_t* stage1;        // [B, K]
+  uint32_t* thresh;       // [B]: T1
+  uint32_t* lists2_rec;   // [B, pair_blocks, pitch2]
+  uint32_t* count2;       // [B, pair_blocks]
+  uint32_t* out;          // [B, K, 6] fp32 bits
+  thin_select_trace tr;
+};
+
+// Number of records in buf[0, n) below x, buf 16-byte aligned with kPad up to
+// the next multiple of 4 (vector loads, no dependent chain).
+__device__ __forceinline__ uint32_t count_below(const uint32_t* buf, uint32_t n, uint32_t x) {
+  const u4v* v = reinterpret_cast<const u4v*>(buf);
+  const uint32_t n4 = (n + 3) / 4;
+  uint32_t c = 0;
+  for (uint32_t u = 0; u < n4; u += 4) {  // four independent loads per step
+    u4v q[4];
+#pragma unroll
+    for (uint32_t h = 0; h < 4; ++h) q[h] = u + h < n4 ? v[u + h] : (u4v)kPad;
+#pragma unroll
+    for (uint32_t h = 0; h < 4; ++h) c += (q[h].x < x) + (q[h].y < x) + (q[h].z < x) + (q[h].w < x);
+  }
+  return c;
+}
+
+// Sorts the n unique records of buf (kPad up to a multiple of 4) by rank
+// counting: out[rank] = record for ranks below `keep`.  Each record is
+// compared by max(1, blockDim / n) threads, each over a slice of buf; their
+// counts meet in ranks[] (n words, LDS).  Every thread of the block calls it;
+// ends with a block barrier.
+__device__ __forceinline__ void rank_sort(const uint32_t* buf, uint32_t n, uint32_t keep, uint32_t* ranks,
+                                          uint32_t* out) {
+  const uint32_t tid = threadIdx.x, bd = blockDim.x;
+  for (uint32_t i = tid; i < n; i += bd) ranks[i] = 0;
+  __syncthreads();
+  const uint32_t n4 = (n + 3) / 4;
+  const uint32_t parts = n ? max(1u, bd / n) : 1u;
+  const uint32_t per = (n4 + parts - 1) / parts;
+  const u4v* v = reinterpret_cast<const u4v*>(buf);
+  for (uint32_t w = tid; w < n * parts; w += bd) {
+    const uint32_t part = w / n, r = w - part * n;
+    const uint32_t mine = buf[r];
+    uint32_t c = 0;
+    const uint32_t hi = min(n4, part * per + per);
+    for (uint32_t u = part * per; u < hi; u += 4) {  // four independent loads per step
+      u4v q[4];
+#pragma unroll
+      for (uint32_t h = 0; h < 4; ++h) q[h] = u + h < hi ? v[u + h] : (u4v)kPad;
+#pragma unroll
+      for (uint32_t h = 0; h < 4; ++h) c += (q[h].x < mine) + (q[h].y < mine) + (q[h].z < mine) + (q[h].w < mine);
+    }
+    if (c) atomicAdd(&ranks[r], c);
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < n; i += bd)
+    if (ranks[i] < keep) out[ranks[i]] = buf[i];
+  __syncthreads();
+}
+
+// Class max of one slice, then the slice's records sorted.  Two load forms:
+// scalar (any strides: a lane per anchor, four class groups per anchor) and,
+// when anchors are contiguous in 16-byte groups (the production [B,4+nc,A]
+// layout read through its [B,A,4+nc] view), a 16-byte load of eight anchors
+// per lane and class, 32 class groups per octet of anchors.  The class groups
+// meet in LDS, where the packed (key << 16 | class) minimum keeps the first
+// class with the best key.
+__global__ __launch_bounds__(1024) void slice_kernel(SplitPlan p) {
+  constexpr uint32_t kGroups = 4;       // scalar form: class groups per anchor
+  constexpr uint32_t kUnroll = 16;      // scalar form: class loads in flight per lane
+  constexpr uint32_t kVGroups = 32;     // vector form: class groups per octet
+  constexpr uint32_t kVUnroll = 4;      // vector form: 16-byte loads in flight per lane
+  __shared__ uint32_t g_kc[kVGroups * kSlice];
+  __shared__ uint16_t g_bits[kVGroups * kSlice];
+  __shared__ __attribute__((aligned(16))) uint32_t recs[kSlice];
+  __shared__ uint32_t ranks[kSlice], sorted[kSlice];
+  const uint32_t b = blockIdx.y, slice = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* img = p.L.x + b * p.L.sb;
+  const uint32_t sc = (uint32_t)p.L.sc;
+  uint32_t groups;
+  if (p.vec_classes) {
+    const uint32_t o = tid & 31u, g = tid >> 5;
+    const uint32_t a0 = slice * kSlice + o * 8u;
+    uint32_t kc[8], bits[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kc[j] = kPad;
+      bits[j] = 0;
+    }
+    if (a0 < p.A) {  // A % 8 == 0: the octet is whole
+      for (uint32_t c0 = g; c0 < p.nc; c0 += kVGroups * kVUnroll) {
+        u4v v[kVUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kVUnroll; ++u) {
+          const uint32_t c = c0 + u * kVGroups;
+          v[u] = c < p.nc ? *reinterpret_cast<const u4v*>(img + (4u + c) * sc + a0) : (u4v)0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kVUnroll; ++u) {
+          const uint32_t c = c0 + u * kVGroups;
+          if (c < p.nc) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t h = (v[u][j / 2] >> (16 * (j & 1))) & 0xffffu;
+              const uint32_t k = (score_key(h) << 16) | c;
+              if (k < kc[j]) {
+                kc[j] = k;
+                bits[j] = h;
+              }
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g_kc[g * kSlice + o * 8 + j] = kc[j];
+      g_bits[g * kSlice + o * 8 + j] = (uint16_t)bits[j];
+    }
+    groups = kVGroups;
+  } else {
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t local = (wave % kGroups) * 64u + lane, grp = wave / kGroups;
+    const uint32_t a = slice * kSlice + local;
+    uint32_t best = kPad, bb = 0u;
+    if (a < p.A) {
+      // one image spans fewer than 2^31 elements (checked on the host)
+      const uint32_t row = a * (uint32_t)p.L.sa + 4u * sc;
+      for (uint32_t c0 = grp; c0 < p.nc; c0 += kGroups * kUnroll) {
+        uint32_t bits[kUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kUnroll; ++u) {
+          const uint32_t c = c0 + u * kGroups;
+          bits[u] = c < p.nc ? img[row + c * sc] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kUnroll; ++u) {
+          const uint32_t c = c0 + u * kGroups;
+          const uint32_t k = c < p.nc ? (score_key(bits[u]) << 16) | c : kPad;
+          if (k < best) {
+            best = k;
+            bb = bits[u];
+          }
+        }
+      }
+    }
+    g_kc[grp * kSlice + local] = best;
+    g_bits[grp * kSlice + local] = (uint16_t)bb;
+    groups = kGroups;
+  }
+  __syncthreads();
+  if (tid < kSlice) {
+    const uint32_t a = slice * kSlice + tid;
+    uint32_t best = g_kc[tid], bb = g_bits[tid];
+    for (uint32_t g = 1; g < groups; ++g) {
+      const uint32_t k = g_kc[g * kSlice + tid];
+      if (k < best) {
+        best = k;
+        bb = g_bits[g * kSlice + tid];
+      }
+    }
+    uint32_t rec = kPad;
+    if (a < p.A) {
+      const size_t t = (size_t)b * p.A + a;
+      p.bits1[t] = (uint16_t)bb;
+      p.cls1[t] = (int32_t)(best & 0xffffu);
+      if (p.tr.class_max) static_cast<uint16_t*>(p.tr.class_max)[t] = (uint16_t)bb;
+      rec = (best & 0xffff0000u) | a;
+    }
+    recs[tid] = rec;
+  }
+  __syncthreads();
+  const uint32_t n = min(kSlice, p.A - slice * kSlice);
+  rank_sort(recs, n, n, ranks, sorted);
+  if (tid < kSlice) p.lists1_rec[((size_t)b * p.lists1 + slice) * kSlice + tid] = tid < n ? sorted[tid] : kPad;
+}
+
+// Merge candidates of `nl` sorted lists held in LDS (list l at lists + l *
+// pitch, length len[l], kPad beyond): cnt[l] records of list l are at most R
+// (see above); they are copied to cand[off[l] ...], their list to from[...];
+// off[nl] is the total.  q: the prefix length (0: choose it here).  Ends with
+// a block barrier.
+__device__ __forceinline__ void merge_candidates(const uint32_t* lists, uint32_t pitch, const uint32_t* len,
+                                                 uint32_t nl, uint32_t K, uint32_t q, uint32_t* cnt, uint32_t* off,
+                                                 uint32_t* cand, uint8_t* from) {
+  const uint32_t tid = threadIdx.x;
+  if (tid < 64) {
+    if (q == 0) {
+      // lane i tries q0 + i * step (q0 = ceil(K / nl)); the first lane whose
+      // prefixes hold K records wins.  Lane 63 tries q >= K, which always holds.
+      const uint32_t q0 = (K + nl - 1) / nl;
+      const uint32_t step = max(1u, (K - min(K, q0) + 62u) / 63u);
+      const uint32_t qi = min(K, q0 + tid * step);
+      uint32_t sum = 0;
+      for (uint32_t l = 0; l < nl; ++l) sum += min(qi, len[l]);
+      const uint64_t ok = __ballot(sum >= K);
+      q = (uint32_t)__shfl((int)qi, __builtin_ctzll(ok), 64);
+    }
+    // the bound R: the largest prefix end
+    const uint32_t m = tid < nl ? min(q, len[tid]) : 0u;
+    uint32_t R = m ? lists[tid * pitch + m - 1] : 0u;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) R = max(R, (uint32_t)__shfl_xor((int)R, o, 64));
+    // cnt: records <= R, at least m; scan 16 at a time past the prefix
+    uint32_t c = m;
+    if (tid < nl) {
+      const uint32_t* lp = lists + tid * pitch;
+      for (;;) {
+        const uint32_t c4 = c & ~3u;
+        uint32_t hit = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+          const uint32_t at = c4 + 4 * u;
+          const u4v v = at < len[tid] ? reinterpret_cast<const u4v*>(lp)[at / 4] : (u4v)kPad;
+          hit += (v.x <= R) + (v.y <= R) + (v.z <= R) + (v.w <= R);
+        }
+        const uint32_t before = c - c4;  // records of the first vector already counted
+        const uint32_t found = hit - min(hit, before);
+        c += found;
+        if (found < 16 - before || c >= len[tid]) break;
+      }
+      c = min(c, len[tid]);
+      cnt[tid] = c;
+    }
+    uint32_t incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_up((int)incl, o, 64);
+      if (tid >= (uint32_t)o) incl += y;
+    }
+    if (tid < nl) off[tid] = incl - c;
+    if (tid == 63) off[nl] = incl;
+  }
+  __syncthreads();
+  // copy each list's candidates; wave w takes lists w, w + 16, ...
+  const uint32_t lane = tid & 63u;
+  for (uint32_t l = tid >> 6; l < nl; l += blockDim.x >> 6)
+    for (uint32_t i = lane; i < cnt[l]; i += 64) {
+      cand[off[l] + i] = lists[l * pitch + i];
+      from[off[l] + i] = (uint8_t)l;
+    }
+  __syncthreads();
+}
+
+// Ranks this block's share of the candidates.  A group of G lanes (G the
+// power of two >= nl, at most 32) takes one candidate; lane o counts the
+// candidates below it in lists o, o + G, ... (its own list: its position), and
+// the counts add up across the group to the candidate's rank.  Calls
+// emit(rank, rec) for ranks below K.  Rounds are wave-uniform, so the
+// shuffles always see their whole group.
+template <typename Emit>
+__device__ __forceinline__ void rank_candidates(const uint32_t* lists, uint32_t pitch, const uint32_t* cnt,
+                                                const uint32_t* off, const uint32_t* cand, const uint8_t* from,
+                                                uint32_t nl, uint32_t K, Emit emit) {
+  uint32_t G = 1;
+  while (G < nl && G < 32) G <<= 1;
+  const uint32_t C = off[nl];
+  const uint32_t share = (C + gridDim.x - 1) / gridDim.x;
+  const uint32_t j0 = blockIdx.x * share, j1 = min(C, j0 + share);
+  const uint32_t groups = blockDim.x / G, group = threadIdx.x / G, o0 = threadIdx.x % G;
+  for (uint32_t base = j0; base < j1; base += groups) {
+    const uint32_t j = base + group;
+    const bool valid = j < j1;
+    uint32_t rec = 0, below = 0;
+    if (valid) {
+      rec = cand[j];
+      const uint32_t l = from[j];
+      for (uint32_t o = o0; o < nl; o += G)
+        below += o == l ? j - off[l] : count_below(lists + o * pitch, cnt[o], rec);
+    }
+    for (uint32_t w = G >> 1; w > 0; w >>= 1) below += (uint32_t)__shfl_xor((int)below, (int)w, 64);
+    if (valid && o0 == 0 && below < K) emit(below, rec);
+  }
+}
+
+// Output row r of batch b: anchor a, label, score bits.
+__device__ __forceinline__ void pack_out(const SplitPlan& p, uint32_t b, uint32_t r, int64_t a, int64_t label,
+                                         uint32_t sbits, int64_t stage2) {
+  const uint16_t* bx = p.L.x + b * p.L.sb + a * p.L.sa;
+  const size_t t = (size_t)b * p.K + r;
+  uint32_t* o = p.out + t * 6;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) o[c] = float_bits(bx[c * p.L.sc]);
+  o[4] = float_bits(sbits);
+  o[5] = __float_as_uint((float)label);
+  if (p.tr.stage2 && stage2 >= 0) static_cast<int64_t*>(p.tr.stage2)[t] = stage2;
+  if (p.tr.anchors) static_cast<int64_t*>(p.tr.anchors)[t] = a;
+  if (p.tr.labels) static_cast<int64_t*>(p.tr.labels)[t] = label;
+  if (p.tr.top_values) static_cast<uint16_t*>(p.tr.top_values)[t] = (uint16_t)sbits;
+}
+
+__global__ __launch_bounds__(1024) void merge1_kernel(SplitPlan p) {
+  __shared__ __attribute__((aligned(16))) uint32_t lists[kMaxLists * kSliceLds];
+  __shared__ uint32_t cand[kMaxLists * kSlice];
+  __shared__ uint8_t from[kMaxLists * kSlice];
+  __shared__ uint32_t len[kMaxLists], cnt[kMaxLists], off[kMaxLists + 1];
+  const uint32_t b = blockIdx.y, tid = threadIdx.x;
+  const uint32_t nl = p.lists1, total = nl * kSlice;
+  const u4v* src = reinterpret_cast<const u4v*>(p.lists1_rec + (size_t)b * total);
+  for (uint32_t v = tid; v < total / 4; v += blockDim.x) {
+    const uint32_t l = v / (kSlice / 4), i4 = v - l * (kSlice / 4);
+    reinterpret_cast<u4v*>(lists)[l * (kSliceLds / 4) + i4] = src[v];
+  }
+  if (tid < nl) len[tid] = min(kSlice, p.A - tid * kSlice);
+  __syncthreads();
+  merge_candidates(lists, kSliceLds, len, nl, p.K, p.q1, cnt, off, cand, from);
+  rank_candidates(lists, kSliceLds, cnt, off, cand, from, nl, p.K, [&](uint32_t rank, uint32_t rec) {
+    const uint32_t a = rec & 0xffffu;
+    const size_t t = (size_t)b * p.K + rank;
+    if (p.tr.stage1) static_cast<int64_t*>(p.tr.stage1)[t] = a;
+    if (p.agnostic) {
+      const size_t ba = (size_t)b * p.A + a;
+      pack_out(p, b, rank, a, p.cls1[ba], p.bits1[ba], -1);
+    } else {
+      p.stage1[t] = (int32_t)a;
+      if (rank == p.K - 1) p.thresh[b] = rec >> 16;
+    }
+  });
+}
+
+__global__ __launch_bounds__(1024) void pairs_kernel(SplitPlan p) {
+  __shared__ __attribute__((aligned(16))) uint32_t surv[kPairCap];
+  __shared__ uint32_t ranks[kPairCap];
+  __shared__ uint32_t sorted[kSplitMaxK];
+  __shared__ int32_t anchors[kSplitMaxK];
+  __shared__ uint32_t s_count;
+  const uint32_t b = blockIdx.y, tid = threadIdx.x;
+  const uint32_t r0 = blockIdx.x * p.ranks_per, r1 = min(p.K, r0 + p.ranks_per);
+  const uint32_t nr = r1 > r0 ? r1 - r0 : 0u;
+  const uint32_t T1 = p.thresh[b];
+  if (tid == 0) s_count = 0;
+  for (uint32_t r = tid; r < nr; r += blockDim.x) anchors[r] = p.stage1[(size_t)b * p.K + r0 + r];
+  __syncthreads();
+  const uint32_t pairs = nr * p.nc;
+  for (uint32_t j = tid; j < pairs; j += blockDim.x) {
+    const uint32_t rr = j / p.nc, c = j - rr * p.nc;
+    const uint32_t bits = p.L.x[b * p.L.sb + (int64_t)anchors[rr] * p.L.sa + (int64_t)(4 + c) * p.L.sc];
+    const uint32_t flat = (r0 + rr) * p.nc + c;
+    if (p.tr.gathered) static_cast<uint16_t*>(p.tr.gathered)[(size_t)b * p.K * p.nc + flat] = (uint16_t)bits;
+    const uint32_t k = score_key(bits);
+    if (k <= T1) surv[atomicAdd(&s_count, 1u)] = (k << 16) | flat;
+  }
+  __syncthreads();
+  const uint32_t n = s_count, keep = min(n, p.K);
+  if (tid < 4 && n + tid < kPairCap) surv[n + tid] = kPad;  // pad to a whole vector
+  __syncthreads();
+  rank_sort(surv, n, keep, ranks, sorted);
+  uint32_t* dst = p.lists2_rec + ((size_t)b * p.pair_blocks + blockIdx.x) * p.pitch2;
+  for (uint32_t i = tid; i < keep; i += blockDim.x) dst[i] = sorted[i];
+  if (tid == 0) p.count2[(size_t)b * p.pair_blocks + blockIdx.x] = keep;
+}
+
+__global__ __launch_bounds__(1024) void merge2_kernel(SplitPlan p) {
+  __shared__ __attribute__((aligned(16))) uint32_t lists[kMerge2Words];
+  __shared__ uint32_t cand[kMerge2Words];
+  __shared__ uint8_t from[kMerge2Words];
+  __shared__ uint32_t len[kMaxLists], cnt[kMaxLists], off[kMaxLists + 1];
+  __shared__ int32_t anchors[kSplitMaxK];
+  const uint32_t b = blockIdx.y, tid = threadIdx.x;
+  const uint32_t nl = p.pair_blocks, pl = p.lds_pitch2;
+  const uint32_t* src = p.lists2_rec + (size_t)b * nl * p.pitch2;
+  if (tid < nl) len[tid] = p.count2[(size_t)b * nl + tid];
+  for (uint32_t r = tid; r < p.K; r += blockDim.x) anchors[r] = p.stage1[(size_t)b * p.K + r];
+  __syncthreads();
+  for (uint32_t v = tid; v < nl * pl; v += blockDim.x) {
+    const uint32_t l = v / pl, i = v - l * pl;
+    lists[v] = i < len[l] ? src[l * p.pitch2 + i] : kPad;
+  }
+  __syncthreads();
+  merge_candidates(lists, pl, len, nl, p.K, 0, cnt, off, cand, from);
+  rank_candidates(lists, pl, cnt, off, cand, from, nl, p.K, [&](uint32_t rank, uint32_t rec) {
+    const uint32_t flat = rec & 0xffffu;
+    const uint32_t r1 = flat / p.nc, c = flat - r1 * p.nc;
+    const int64_t a = anchors[r1];
+    const uint32_t sbits = p.L.x[b * p.L.sb + a * p.L.sa + (int64_t)(4 + c) * p.L.sc];
+    pack_out(p, b, rank, a, c, sbits, flat);
+  });
+}
+
 // ---------------------------------------------------------------- host
 
+// Shape of the split selection for these sizes; ok == false leaves them to
+// the one-workgroup-per-batch path (more anchors than 64 lists of kSlice,
+// K above kSplitMaxK, or pair indices / pair lists too large).
+struct SplitShape {
+  bool ok;
+  uint32_t lists1, q1, pair_blocks, ranks_per, pitch2, lds_pitch2;
+};
+
+SplitShape split_shape(int64_t B, int64_t A, int64_t nc, int64_t K, bool agnostic, int64_t image_extent) {
+  SplitShape sh;
+  memset(&sh, 0, sizeof sh);
+  if (K < 1 || K > (int64_t)kSplitMaxK || A > (int64_t)(kMaxLists * kSlice) || B > 65535 ||
+      image_extent >= ((int64_t)1 << 31))
+    return sh;
+  sh.lists1 = (uint32_t)((A + kSlice - 1) / kSlice);
+  // q1: the smallest prefix length whose lists' prefixes hold K records
+  for (uint32_t q = 1; q <= kSlice; ++q) {
+    int64_t sum = 0;
+    for (uint32_t l = 0; l < sh.lists1; ++l) sum += std::min<int64_t>(q, A - (int64_t)l * kSlice);
+    if (sum >= K) {
+      sh.q1 = q;
+      break;
+    }
+  }
+  if (!agnostic) {
+    if (K * nc > 65536) return sh;
+    const int64_t per = std::max<int64_t>(1, std::min<int64_t>(K, 2048 / nc));
+    if (per * nc > (int64_t)kPairCap) return sh;
+    sh.ranks_per = (uint32_t)per;
+    sh.pair_blocks = (uint32_t)((K + per - 1) / per);
+    sh.pitch2 = (uint32_t)((K + 3) & ~(int64_t)3);
+    sh.lds_pitch2 = (uint32_t)(((K + 63) & ~(int64_t)63) + 4);
+    if (sh.pair_blocks > kMaxLists || (int64_t)sh.pair_blocks * sh.lds_pitch2 > (int64_t)kMerge2Words) return sh;
+  }
+  sh.ok = true;
+  return sh;
+}
+
 struct WsLayout {
-  size_t bits1, cls1, stage1, gathered, stage2, thresh, recs, total;
+  size_t bits1, cls1, stage1, gathered, stage2, thresh, recs, lists1, lists2, count2, total;
   uint32_t recs_pitch;  // P for the large-K path (0 = not needed)
+  SplitShape split;
 };
 
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-WsLayout ws_layout(int64_t B, int64_t A, int64_t nc, int64_t max_det, bool agnostic) {
+// image_extent: elements one image of `decoded` spans (its largest offset + 1);
+// -1 when unknown (workspace queries size for the split path whenever it
+// could apply).
+WsLayout ws_layout(int64_t B, int64_t A, int64_t nc, int64_t max_det, bool agnostic, int64_t image_extent = -1) {
   WsLayout w;
   memset(&w, 0, sizeof w);
   const int64_t K = max_det < A ? max_det : A;
+  w.split = split_shape(B, A, nc, K, agnostic, image_extent < 0 ? 0 : image_extent);
   size_t off = 0;
   w.bits1 = off; off += up256((size_t)(B * A) * 2);
   w.cls1 = off; off += up256((size_t)(B * A) * 4);
@@ -715,6 +1194,13 @@ WsLayout ws_layout(int64_t B, int64_t A, int64_t nc, int64_t max_det, bool agnos
     w.gathered = off; off += up256((size_t)(B * K * nc) * 2);
     w.stage2 = off; off += up256((size_t)(B * K) * 4);
     w.thresh = off; off += up256((size_t)B * 4);
+  }
+  if (w.split.ok) {
+    w.lists1 = off; off += up256((size_t)B * w.split.lists1 * kSlice * 4);
+    if (!agnostic) {
+      w.lists2 = off; off += up256((size_t)B * w.split.pair_blocks * (size_t)w.split.pitch2 * 4);
+      w.count2 = off; off += up256((size_t)B * w.split.pair_blocks * 4);
+    }
   }
   if (K > (int64_t)kLdsSort) {
     const int64_t n = agnostic ? A : (A > K * nc ? A : K * nc);
@@ -770,6 +1256,11 @@ extern "C" size_t thin_detection_select_workspace(int64_t batches, int64_t ancho
 namespace thin {
 namespace {
 
+// Elements one image of decoded [B, A, 4+nc] spans: its largest offset + 1.
+int64_t image_extent(const thin_desc* d) {
+  return 1 + (d->sizes[1] - 1) * d->strides[1] + (d->sizes[2] - 1) * d->strides[2];
+}
+
 // Argument checks shared by both entry points.  Sets *skip when the call has
 // nothing to launch (empty batch or anchors, or K == 0 without a class_max
 // trace: selection_flow.cpp:436-439).
@@ -812,6 +1303,44 @@ thin_status select_run(const thin_desc* decoded, int64_t max_det, bool agn, void
 
   Layout L{static_cast<const uint16_t*>(decoded->data), decoded->strides[0], decoded->strides[1],
            decoded->strides[2]};
+  if (w.split.ok) {
+    SplitPlan sp;
+    memset(&sp, 0, sizeof sp);
+    sp.L = L;
+    sp.A = (uint32_t)A;
+    sp.nc = (uint32_t)nc;
+    sp.K = (uint32_t)K;
+    sp.lists1 = w.split.lists1;
+    sp.q1 = w.split.q1;
+    sp.pair_blocks = w.split.pair_blocks;
+    sp.ranks_per = w.split.ranks_per;
+    sp.pitch2 = w.split.pitch2;
+    sp.lds_pitch2 = w.split.lds_pitch2;
+    sp.agnostic = agn ? 1 : 0;
+    sp.vec_classes = decoded->strides[1] == 1 && A % 8 == 0 && decoded->strides[2] % 8 == 0 &&
+                     (B == 1 || decoded->strides[0] % 8 == 0) &&
+                     reinterpret_cast<uintptr_t>(decoded->data) % 16 == 0;
+    sp.bits1 = bits1;
+    sp.cls1 = cls1;
+    sp.lists1_rec = reinterpret_cast<uint32_t*>(ws + w.lists1);
+    sp.stage1 = stage1;
+    sp.thresh = agn ? nullptr : reinterpret_cast<uint32_t*>(ws + w.thresh);
+    sp.lists2_rec = agn ? nullptr : reinterpret_cast<uint32_t*>(ws + w.lists2);
+    sp.count2 = agn ? nullptr : reinterpret_cast<uint32_t*>(ws + w.count2);
+    sp.out = static_cast<uint32_t*>(out);
+    sp.tr = tr;
+    const uint32_t nb = (uint32_t)B;
+    hipLaunchKernelGGL(slice_kernel, dim3(sp.lists1, nb), dim3(1024), 0, stream, sp);
+    THIN_LAUNCH_CHECK("select_slice");
+    hipLaunchKernelGGL(merge1_kernel, dim3(kMergeBlocks, nb), dim3(1024), 0, stream, sp);
+    THIN_LAUNCH_CHECK("select_merge1");
+    if (agn) return THIN_OK;
+    hipLaunchKernelGGL(pairs_kernel, dim3(sp.pair_blocks, nb), dim3(1024), 0, stream, sp);
+    THIN_LAUNCH_CHECK("select_pairs");
+    hipLaunchKernelGGL(merge2_kernel, dim3(kMergeBlocks, nb), dim3(1024), 0, stream, sp);
+    THIN_LAUNCH_CHECK("select_merge2");
+    return THIN_OK;
+  }
   constexpr int kGroups = 16;
   hipLaunchKernelGGL((class_max_wide_kernel<kGroups>), dim3((uint32_t)((B * A + 63) / 64)), dim3(64 * kGroups), 0,
                      stream, L, B, A, nc, bits1, cls1, static_cast<uint16_t*>(tr.class_max));
@@ -893,7 +1422,8 @@ extern "C" thin_status thin_detection_select(const thin_desc* decoded, int64_t m
   thin_status s = select_validate(decoded, max_det, out, trace, &skip);
   if (s != THIN_OK || skip) return s;
   const bool agn = agnostic != 0;
-  const WsLayout w = ws_layout(decoded->sizes[0], decoded->sizes[1], decoded->sizes[2] - 4, max_det, agn);
+  const WsLayout w = ws_layout(decoded->sizes[0], decoded->sizes[1], decoded->sizes[2] - 4, max_det, agn,
+                               image_extent(decoded));
   THIN_REQUIRE(workspace != nullptr && workspace_bytes >= w.total, THIN_ERR_WORKSPACE,
                "detection_select: workspace of %zu bytes needed, %zu given", w.total, workspace_bytes);
   THIN_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, THIN_ERR_WORKSPACE,
@@ -943,7 +1473,8 @@ extern "C" thin_status thin_detection_select_noalloc(const thin_desc* decoded, i
   thin_status s = select_validate(decoded, max_det, out, trace, &skip);
   if (s != THIN_OK || skip) return s;
   const bool agn = agnostic != 0;
-  const WsLayout w = ws_layout(decoded->sizes[0], decoded->sizes[1], decoded->sizes[2] - 4, max_det, agn);
+  const WsLayout w = ws_layout(decoded->sizes[0], decoded->sizes[1], decoded->sizes[2] - 4, max_det, agn,
+                               image_extent(decoded));
   THIN_REQUIRE(w.total <= (size_t)THIN_SELECT_SCRATCH_BYTES, THIN_ERR_WORKSPACE,
                "detection_select_noalloc: these sizes need %zu bytes of scratch, the static scratch holds %zu "
                "(use thin_detection_select with a workspace)",
