@@ -727,11 +727,16 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackArgs p) {
 // short candidate prefixes.
 constexpr uint32_t kSlice = 256;         // anchors per stage-1 list
 constexpr uint32_t kMaxLists = 64;       // lists per batch and stage
-constexpr uint32_t kMergeBlocks = 16;    // merge workgroups per batch
+constexpr uint32_t kMergeBlocks = 32;    // merge workgroups per batch
 constexpr uint32_t kSplitMaxK = 1024;
 constexpr uint32_t kPairCap = 4096;      // gathered pairs per pairs block
 constexpr uint32_t kMerge2Words = 16384; // pair lists per batch: pair_blocks * K records
 constexpr uint32_t kPad = 0xffffffffu;
+// Every split kernel runs 1024-thread workgroups.  Device code uses these
+// constants rather than blockDim / gridDim, which are read from the dispatch's
+// implicit arguments in memory (a dependent load on the critical path).
+constexpr uint32_t kSplitThreads = 1024;
+constexpr uint32_t kSliceThreads = 1024;  // slice_kernel workgroups
 // LDS pitch of a stage-1 list: 260 words puts list l's vectors on banks 4l
 // mod 64 (a 256-word pitch would put every list on the same banks, and the
 // lanes that scan different lists would serialise).
@@ -779,12 +784,14 @@ __device__ __forceinline__ uint32_t count_below(const uint32_t* buf, uint32_t n,
 
 // Sorts the n unique records of buf (kPad up to a multiple of 4) by rank
 // counting: out[rank] = record for ranks below `keep`.  Each record is
-// compared by max(1, blockDim / n) threads, each over a slice of buf; their
+// compared by max(1, BD / n) threads (BD: the block size), each over a slice
+// of buf; their
 // counts meet in ranks[] (n words, LDS).  Every thread of the block calls it;
 // ends with a block barrier.
+template <uint32_t BD>
 __device__ __forceinline__ void rank_sort(const uint32_t* buf, uint32_t n, uint32_t keep, uint32_t* ranks,
                                           uint32_t* out) {
-  const uint32_t tid = threadIdx.x, bd = blockDim.x;
+  const uint32_t tid = threadIdx.x, bd = BD;
   for (uint32_t i = tid; i < n; i += bd) ranks[i] = 0;
   __syncthreads();
   const uint32_t n4 = (n + 3) / 4;
@@ -818,10 +825,12 @@ __device__ __forceinline__ void rank_sort(const uint32_t* buf, uint32_t n, uint3
 // per lane and class, 32 class groups per octet of anchors.  The class groups
 // meet in LDS, where the packed (key << 16 | class) minimum keeps the first
 // class with the best key.
-__global__ __launch_bounds__(1024) void slice_kernel(SplitPlan p) {
-  constexpr uint32_t kGroups = 4;       // scalar form: class groups per anchor
+__global__ __launch_bounds__(kSliceThreads) void slice_kernel(SplitPlan p) {
+  constexpr uint32_t kTiles = kSlice / 64;                  // scalar form: 64-anchor tiles
+  constexpr uint32_t kGroups = kSliceThreads / kSlice;      // scalar form: class groups per anchor
   constexpr uint32_t kUnroll = 16;      // scalar form: class loads in flight per lane
-  constexpr uint32_t kVGroups = 32;     // vector form: class groups per octet
+  constexpr uint32_t kOctets = kSlice / 8;
+  constexpr uint32_t kVGroups = kSliceThreads / kOctets;   // vector form: class groups per octet
   constexpr uint32_t kVUnroll = 4;      // vector form: 16-byte loads in flight per lane
   __shared__ uint32_t g_kc[kVGroups * kSlice];
   __shared__ uint16_t g_bits[kVGroups * kSlice];
@@ -832,7 +841,7 @@ __global__ __launch_bounds__(1024) void slice_kernel(SplitPlan p) {
   const uint32_t sc = (uint32_t)p.L.sc;
   uint32_t groups;
   if (p.vec_classes) {
-    const uint32_t o = tid & 31u, g = tid >> 5;
+    const uint32_t o = tid % kOctets, g = tid / kOctets;
     const uint32_t a0 = slice * kSlice + o * 8u;
     uint32_t kc[8], bits[8];
 #pragma unroll
@@ -873,7 +882,7 @@ __global__ __launch_bounds__(1024) void slice_kernel(SplitPlan p) {
     groups = kVGroups;
   } else {
     const uint32_t lane = tid & 63u, wave = tid >> 6;
-    const uint32_t local = (wave % kGroups) * 64u + lane, grp = wave / kGroups;
+    const uint32_t local = (wave % kTiles) * 64u + lane, grp = wave / kTiles;
     const uint32_t a = slice * kSlice + local;
     uint32_t best = kPad, bb = 0u;
     if (a < p.A) {
@@ -924,8 +933,45 @@ __global__ __launch_bounds__(1024) void slice_kernel(SplitPlan p) {
   }
   __syncthreads();
   const uint32_t n = min(kSlice, p.A - slice * kSlice);
-  rank_sort(recs, n, n, ranks, sorted);
+  rank_sort<kSliceThreads>(recs, n, n, ranks, sorted);
   if (tid < kSlice) p.lists1_rec[((size_t)b * p.lists1 + slice) * kSlice + tid] = tid < n ? sorted[tid] : kPad;
+}
+
+// Wave-wide max and inclusive prefix sum by DPP row operations and the
+// gfx950 permlane swaps (VALU only; a ds_bpermute shuffle costs ~150 cycles
+// per dependent step, these a few each).
+__device__ __forceinline__ uint32_t xor16(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16u) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t xor32(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32u) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true));   // xor 1
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true));   // xor 2
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x124, 0xF, 0xF, true));  // row_ror:4
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, true));  // row_ror:8
+  v = max(v, xor16(v));
+  return max(v, xor32(v));
+}
+// Inclusive prefix sum across the wave's 64 lanes.
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+  const uint32_t lane = threadIdx.x & 63u;
+  // within rows of 16: shifts by 1, 2, 4, 8 (lanes shifted in from outside the row add 0)
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  // across rows: add the total of every earlier row
+  const uint32_t row_total = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+  const uint32_t t1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t t2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 47);
+  v += lane >= 16 ? row_total : 0u;
+  v += lane >= 32 ? t1 : 0u;
+  v += lane >= 48 ? t2 : 0u;
+  return v;
 }
 
 // Merge candidates of `nl` sorted lists held in LDS (list l at lists + l *
@@ -937,7 +983,7 @@ __device__ __forceinline__ void merge_candidates(const uint32_t* lists, uint32_t
                                                  uint32_t nl, uint32_t K, uint32_t q, uint32_t* cnt, uint32_t* off,
                                                  uint32_t* cand, uint8_t* from) {
   const uint32_t tid = threadIdx.x;
-  if (tid < 64) {
+  if (tid < 64) {  // wave 0; lane t handles lists t and t + 64
     if (q == 0) {
       // lane i tries q0 + i * step (q0 = ceil(K / nl)); the first lane whose
       // prefixes hold K records wins.  Lane 63 tries q >= K, which always holds.
@@ -950,44 +996,52 @@ __device__ __forceinline__ void merge_candidates(const uint32_t* lists, uint32_t
       q = (uint32_t)__shfl((int)qi, __builtin_ctzll(ok), 64);
     }
     // the bound R: the largest prefix end
-    const uint32_t m = tid < nl ? min(q, len[tid]) : 0u;
-    uint32_t R = m ? lists[tid * pitch + m - 1] : 0u;
+    uint32_t m[2], R = 0;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) R = max(R, (uint32_t)__shfl_xor((int)R, o, 64));
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t l = tid + 64 * h;
+      m[h] = l < nl ? min(q, len[l]) : 0u;
+      if (m[h]) R = max(R, lists[l * pitch + m[h] - 1]);
+    }
+    R = wave_max_u32(R);
     // cnt: records <= R, at least m; scan 16 at a time past the prefix
-    uint32_t c = m;
-    if (tid < nl) {
-      const uint32_t* lp = lists + tid * pitch;
-      for (;;) {
-        const uint32_t c4 = c & ~3u;
-        uint32_t hit = 0;
+    uint32_t c[2];
 #pragma unroll
-        for (uint32_t u = 0; u < 4; ++u) {
-          const uint32_t at = c4 + 4 * u;
-          const u4v v = at < len[tid] ? reinterpret_cast<const u4v*>(lp)[at / 4] : (u4v)kPad;
-          hit += (v.x <= R) + (v.y <= R) + (v.z <= R) + (v.w <= R);
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t l = tid + 64 * h;
+      c[h] = m[h];
+      if (l < nl) {
+        const uint32_t* lp = lists + l * pitch;
+        const uint32_t n = len[l];
+        for (;;) {
+          const uint32_t c4 = c[h] & ~3u;
+          uint32_t hit = 0;
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t at = c4 + 4 * u;
+            const u4v v = at < n ? reinterpret_cast<const u4v*>(lp)[at / 4] : (u4v)kPad;
+            hit += (v.x <= R) + (v.y <= R) + (v.z <= R) + (v.w <= R);
+          }
+          const uint32_t before = c[h] - c4;  // records of the first vector already counted
+          const uint32_t found = hit - min(hit, before);
+          c[h] += found;
+          if (found < 16 - before || c[h] >= n) break;
         }
-        const uint32_t before = c - c4;  // records of the first vector already counted
-        const uint32_t found = hit - min(hit, before);
-        c += found;
-        if (found < 16 - before || c >= len[tid]) break;
+        c[h] = min(c[h], n);
+        cnt[l] = c[h];
       }
-      c = min(c, len[tid]);
-      cnt[tid] = c;
     }
-    uint32_t incl = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = (uint32_t)__shfl_up((int)incl, o, 64);
-      if (tid >= (uint32_t)o) incl += y;
-    }
-    if (tid < nl) off[tid] = incl - c;
-    if (tid == 63) off[nl] = incl;
+    const uint32_t incl0 = wave_scan_u32(c[0]);
+    const uint32_t total0 = (uint32_t)__builtin_amdgcn_readlane((int)incl0, 63);
+    const uint32_t incl1 = wave_scan_u32(c[1]) + total0;
+    if (tid < nl) off[tid] = incl0 - c[0];
+    if (tid + 64 < nl) off[tid + 64] = incl1 - c[1];
+    if (tid == 63) off[nl] = incl1;
   }
   __syncthreads();
   // copy each list's candidates; wave w takes lists w, w + 16, ...
   const uint32_t lane = tid & 63u;
-  for (uint32_t l = tid >> 6; l < nl; l += blockDim.x >> 6)
+  for (uint32_t l = tid >> 6; l < nl; l += kSplitThreads >> 6)
     for (uint32_t i = lane; i < cnt[l]; i += 64) {
       cand[off[l] + i] = lists[l * pitch + i];
       from[off[l] + i] = (uint8_t)l;
@@ -995,22 +1049,30 @@ __device__ __forceinline__ void merge_candidates(const uint32_t* lists, uint32_t
   __syncthreads();
 }
 
-// Ranks this block's share of the candidates.  A group of G lanes (G the
-// power of two >= nl, at most 32) takes one candidate; lane o counts the
-// candidates below it in lists o, o + G, ... (its own list: its position), and
-// the counts add up across the group to the candidate's rank.  Calls
-// emit(rank, rec) for ranks below K.  Rounds are wave-uniform, so the
-// shuffles always see their whole group.
+// Sum over aligned groups of 8 lanes, every lane gets its group's total: xor
+// 1 and 2 by quad permutes, xor 4 by row shifts (DPP, no LDS round trip).
+__device__ __forceinline__ uint32_t group8_sum(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
+  v += (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
+  const uint32_t up = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x104, 0xF, 0xF, true);    // row_shl:4
+  const uint32_t down = (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  return v + ((threadIdx.x & 4u) ? down : up);
+}
+
+// Ranks this block's share of the candidates.  A group of 8 lanes takes one
+// candidate; lane o counts the candidates below it in lists o, o + 8, ...
+// (its own list: its position), and the counts add up across the group to
+// the candidate's rank.  Calls emit(rank, rec) for ranks below K.  Rounds are
+// wave-uniform, so the cross-lane sums always see their whole group.
 template <typename Emit>
 __device__ __forceinline__ void rank_candidates(const uint32_t* lists, uint32_t pitch, const uint32_t* cnt,
                                                 const uint32_t* off, const uint32_t* cand, const uint8_t* from,
                                                 uint32_t nl, uint32_t K, Emit emit) {
-  uint32_t G = 1;
-  while (G < nl && G < 32) G <<= 1;
+  constexpr uint32_t G = 8;
   const uint32_t C = off[nl];
-  const uint32_t share = (C + gridDim.x - 1) / gridDim.x;
+  const uint32_t share = (C + kMergeBlocks - 1) / kMergeBlocks;
   const uint32_t j0 = blockIdx.x * share, j1 = min(C, j0 + share);
-  const uint32_t groups = blockDim.x / G, group = threadIdx.x / G, o0 = threadIdx.x % G;
+  const uint32_t groups = kSplitThreads / G, group = threadIdx.x / G, o0 = threadIdx.x % G;
   for (uint32_t base = j0; base < j1; base += groups) {
     const uint32_t j = base + group;
     const bool valid = j < j1;
@@ -1021,19 +1083,25 @@ __device__ __forceinline__ void rank_candidates(const uint32_t* lists, uint32_t 
       for (uint32_t o = o0; o < nl; o += G)
         below += o == l ? j - off[l] : count_below(lists + o * pitch, cnt[o], rec);
     }
-    for (uint32_t w = G >> 1; w > 0; w >>= 1) below += (uint32_t)__shfl_xor((int)below, (int)w, 64);
+    below = group8_sum(below);
     if (valid && o0 == 0 && below < K) emit(below, rec);
   }
 }
 
 // Output row r of batch b: anchor a, label, score bits.
+// All loads come before any store: a wave waits for its stores as well as its
+// loads when it needs a load result, so interleaving them would serialise on
+// store completion.
 __device__ __forceinline__ void pack_out(const SplitPlan& p, uint32_t b, uint32_t r, int64_t a, int64_t label,
                                          uint32_t sbits, int64_t stage2) {
   const uint16_t* bx = p.L.x + b * p.L.sb + a * p.L.sa;
+  uint32_t box[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) box[c] = bx[c * p.L.sc];
   const size_t t = (size_t)b * p.K + r;
   uint32_t* o = p.out + t * 6;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) o[c] = float_bits(bx[c * p.L.sc]);
+  for (int c = 0; c < 4; ++c) o[c] = float_bits(box[c]);
   o[4] = float_bits(sbits);
   o[5] = __float_as_uint((float)label);
   if (p.tr.stage2 && stage2 >= 0) static_cast<int64_t*>(p.tr.stage2)[t] = stage2;
@@ -1042,7 +1110,7 @@ __device__ __forceinline__ void pack_out(const SplitPlan& p, uint32_t b, uint32_
   if (p.tr.top_values) static_cast<uint16_t*>(p.tr.top_values)[t] = (uint16_t)sbits;
 }
 
-__global__ __launch_bounds__(1024) void merge1_kernel(SplitPlan p) {
+__global__ __launch_bounds__(kSplitThreads) void merge1_kernel(SplitPlan p) {
   __shared__ __attribute__((aligned(16))) uint32_t lists[kMaxLists * kSliceLds];
   __shared__ uint32_t cand[kMaxLists * kSlice];
   __shared__ uint8_t from[kMaxLists * kSlice];
@@ -1050,7 +1118,7 @@ __global__ __launch_bounds__(1024) void merge1_kernel(SplitPlan p) {
   const uint32_t b = blockIdx.y, tid = threadIdx.x;
   const uint32_t nl = p.lists1, total = nl * kSlice;
   const u4v* src = reinterpret_cast<const u4v*>(p.lists1_rec + (size_t)b * total);
-  for (uint32_t v = tid; v < total / 4; v += blockDim.x) {
+  for (uint32_t v = tid; v < total / 4; v += kSplitThreads) {
     const uint32_t l = v / (kSlice / 4), i4 = v - l * (kSlice / 4);
     reinterpret_cast<u4v*>(lists)[l * (kSliceLds / 4) + i4] = src[v];
   }
@@ -1071,7 +1139,7 @@ __global__ __launch_bounds__(1024) void merge1_kernel(SplitPlan p) {
   });
 }
 
-__global__ __launch_bounds__(1024) void pairs_kernel(SplitPlan p) {
+__global__ __launch_bounds__(kSplitThreads) void pairs_kernel(SplitPlan p) {
   __shared__ __attribute__((aligned(16))) uint32_t surv[kPairCap];
   __shared__ uint32_t ranks[kPairCap];
   __shared__ uint32_t sorted[kSplitMaxK];
@@ -1082,10 +1150,10 @@ __global__ __launch_bounds__(1024) void pairs_kernel(SplitPlan p) {
   const uint32_t nr = r1 > r0 ? r1 - r0 : 0u;
   const uint32_t T1 = p.thresh[b];
   if (tid == 0) s_count = 0;
-  for (uint32_t r = tid; r < nr; r += blockDim.x) anchors[r] = p.stage1[(size_t)b * p.K + r0 + r];
+  for (uint32_t r = tid; r < nr; r += kSplitThreads) anchors[r] = p.stage1[(size_t)b * p.K + r0 + r];
   __syncthreads();
   const uint32_t pairs = nr * p.nc;
-  for (uint32_t j = tid; j < pairs; j += blockDim.x) {
+  for (uint32_t j = tid; j < pairs; j += kSplitThreads) {
     const uint32_t rr = j / p.nc, c = j - rr * p.nc;
     const uint32_t bits = p.L.x[b * p.L.sb + (int64_t)anchors[rr] * p.L.sa + (int64_t)(4 + c) * p.L.sc];
     const uint32_t flat = (r0 + rr) * p.nc + c;
@@ -1097,13 +1165,13 @@ __global__ __launch_bounds__(1024) void pairs_kernel(SplitPlan p) {
   const uint32_t n = s_count, keep = min(n, p.K);
   if (tid < 4 && n + tid < kPairCap) surv[n + tid] = kPad;  // pad to a whole vector
   __syncthreads();
-  rank_sort(surv, n, keep, ranks, sorted);
+  rank_sort<kSplitThreads>(surv, n, keep, ranks, sorted);
   uint32_t* dst = p.lists2_rec + ((size_t)b * p.pair_blocks + blockIdx.x) * p.pitch2;
-  for (uint32_t i = tid; i < keep; i += blockDim.x) dst[i] = sorted[i];
+  for (uint32_t i = tid; i < keep; i += kSplitThreads) dst[i] = sorted[i];
   if (tid == 0) p.count2[(size_t)b * p.pair_blocks + blockIdx.x] = keep;
 }
 
-__global__ __launch_bounds__(1024) void merge2_kernel(SplitPlan p) {
+__global__ __launch_bounds__(kSplitThreads) void merge2_kernel(SplitPlan p) {
   __shared__ __attribute__((aligned(16))) uint32_t lists[kMerge2Words];
   __shared__ uint32_t cand[kMerge2Words];
   __shared__ uint8_t from[kMerge2Words];
@@ -1113,9 +1181,9 @@ __global__ __launch_bounds__(1024) void merge2_kernel(SplitPlan p) {
   const uint32_t nl = p.pair_blocks, pl = p.lds_pitch2;
   const uint32_t* src = p.lists2_rec + (size_t)b * nl * p.pitch2;
   if (tid < nl) len[tid] = p.count2[(size_t)b * nl + tid];
-  for (uint32_t r = tid; r < p.K; r += blockDim.x) anchors[r] = p.stage1[(size_t)b * p.K + r];
+  for (uint32_t r = tid; r < p.K; r += kSplitThreads) anchors[r] = p.stage1[(size_t)b * p.K + r];
   __syncthreads();
-  for (uint32_t v = tid; v < nl * pl; v += blockDim.x) {
+  for (uint32_t v = tid; v < nl * pl; v += kSplitThreads) {
     const uint32_t l = v / pl, i = v - l * pl;
     lists[v] = i < len[l] ? src[l * p.pitch2 + i] : kPad;
   }
@@ -1330,14 +1398,14 @@ thin_status select_run(const thin_desc* decoded, int64_t max_det, bool agn, void
     sp.out = static_cast<uint32_t*>(out);
     sp.tr = tr;
     const uint32_t nb = (uint32_t)B;
-    hipLaunchKernelGGL(slice_kernel, dim3(sp.lists1, nb), dim3(1024), 0, stream, sp);
+    hipLaunchKernelGGL(slice_kernel, dim3(sp.lists1, nb), dim3(kSliceThreads), 0, stream, sp);
     THIN_LAUNCH_CHECK("select_slice");
-    hipLaunchKernelGGL(merge1_kernel, dim3(kMergeBlocks, nb), dim3(1024), 0, stream, sp);
+    hipLaunchKernelGGL(merge1_kernel, dim3(kMergeBlocks, nb), dim3(kSplitThreads), 0, stream, sp);
     THIN_LAUNCH_CHECK("select_merge1");
     if (agn) return THIN_OK;
-    hipLaunchKernelGGL(pairs_kernel, dim3(sp.pair_blocks, nb), dim3(1024), 0, stream, sp);
+    hipLaunchKernelGGL(pairs_kernel, dim3(sp.pair_blocks, nb), dim3(kSplitThreads), 0, stream, sp);
     THIN_LAUNCH_CHECK("select_pairs");
-    hipLaunchKernelGGL(merge2_kernel, dim3(kMergeBlocks, nb), dim3(1024), 0, stream, sp);
+    hipLaunchKernelGGL(merge2_kernel, dim3(kMergeBlocks, nb), dim3(kSplitThreads), 0, stream, sp);
     THIN_LAUNCH_CHECK("select_merge2");
     return THIN_OK;
   }
