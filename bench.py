@@ -333,6 +333,58 @@ def op_attn_pv(capi, dev, n, rotate=True):
         sets, algo
 
 
+def attn_fused_bytes():
+    """qkv read once, mixed values written once."""
+    heads, key, dim, tokens = ATTN
+    return (heads * (2 * key + dim) + heads * dim) * tokens * 2
+
+
+def op_attn_fused(capi, dev, n, prescale, rotate=True):
+    """The whole attention chain of one C2PSA block in one launch
+    (thin_attention): qkv [1,32,400,16] -> mixed values [1,16,400,16]; 123
+    MFLOP, bit-equal to the chain below."""
+    heads, key, dim, tokens = ATTN
+    algo = attn_fused_bytes()
+    scale = float(torch.tensor(key ** -0.5, dtype=torch.float64).half())
+    sets = rotated(lambda i: (attn_qkv(dev, 330 + i),
+                              torch.empty((1, heads * dim // 16, tokens, 16), dtype=torch.float16, device=dev)),
+                   algo, rotate)
+    return (lambda st: capi.attention(st[0], heads, key, dim, scale, prescale, out=st[1])), sets, algo
+
+
+def op_attn_chain(capi, dev, n, prescale, rotate=True):
+    """The same chain op by op, as attention_forward runs it: channel_select,
+    mul, layout_bmm (q^T k), row softmax, layout_bmm (v p^T) -- five launches
+    (four in the post-scale form, where the mul follows the product)."""
+    heads, key, dim, tokens = ATTN
+    algo = attn_fused_bytes()
+    scale = float(torch.tensor(key ** -0.5, dtype=torch.float64).half())
+
+    def buffers(i):
+        return (attn_qkv(dev, 340 + i),
+                torch.empty((1, heads * key // 16, tokens, 16), dtype=torch.float16, device=dev),
+                torch.empty((1, heads * key // 16, tokens, 16), dtype=torch.float16, device=dev),
+                torch.empty((heads, tokens, tokens), dtype=torch.float16, device=dev),
+                torch.empty((heads, tokens, tokens), dtype=torch.float16, device=dev),
+                torch.empty((heads, tokens, tokens), dtype=torch.float16, device=dev),
+                torch.empty((1, heads * dim // 16, tokens, 16), dtype=torch.float16, device=dev))
+    sets = rotated(buffers, algo, rotate)
+
+    def run(st):
+        qkv, sel, query, scores, scaled, prob, out = st
+        if prescale:
+            capi.channel_select(qkv, heads, 0, key, out=sel)
+            capi.binary_scalar(capi.MUL, sel, scale, out=query)
+            capi.layout_bmm(query, qkv, True, False, False, heads, 0, key, key, key, out=scores)
+            capi.softmax(scores, 2, out=prob)
+        else:
+            capi.layout_bmm(qkv, qkv, True, False, False, heads, 0, key, key, key, out=scores)
+            capi.binary_scalar(capi.MUL, scores, scale, out=scaled)
+            capi.softmax(scaled, 2, out=prob)
+        capi.layout_bmm(qkv, prob, False, True, True, heads, 2 * key, dim, out=out)
+    return run, sets, algo
+
+
 def op_attn_select(capi, dev, n, rotate=True):
     """channel_select of v (the position branch input): [1,16,400,16] out."""
     heads, key, dim, tokens = ATTN
@@ -384,6 +436,12 @@ def op_rows(capi, dev):
     rows.append(("attn_qk_4x32x400", "ATTN", 1, lambda r: op_attn_qk(capi, dev, 1, r)))
     rows.append(("attn_pv_4x64x400", "ATTN", 1, lambda r: op_attn_pv(capi, dev, 1, r)))
     rows.append(("channel_select_4x64x400", "ATTN", 1, lambda r: op_attn_select(capi, dev, 1, r)))
+    for form in ("prescale", "postscale"):
+        pre = form == "prescale"
+        rows.append((f"attn_fused_{form}_4x32x64x400", "ATTN", 1,
+                     lambda r, pre=pre: op_attn_fused(capi, dev, 1, pre, r)))
+        rows.append((f"attn_chain_{form}_4x32x64x400", "ATTN", 1,
+                     lambda r, pre=pre: op_attn_chain(capi, dev, 1, pre, r)))
     for layout in ("contiguous", "transposed"):
         rows.append((f"detection_select_{layout}", "C5", 1, lambda r, l=layout: op_select(capi, dev, l)))
     return rows
@@ -471,6 +529,20 @@ def cpu_op(name, n):
             p = torch.rand(heads, tokens, tokens, generator=g).half()
             return (lambda: ob.layout_bmm(qkv, p, False, True, True, heads, 2 * key, dim)), \
                 heads * (2 * dim * tokens + tokens * tokens) * 2
+        if name.startswith("attn_fused") or name.startswith("attn_chain"):
+            from oracle import elementwise as ew  # the CPU chain, timed
+            from oracle import reductions as rd
+            pre = "_prescale_" in name
+
+            def attention():
+                if pre:
+                    query = ew.binary_scalar_rounded(1, ob.channel_select(qkv, heads, 0, key), key ** -0.5)
+                    scores = ob.layout_bmm(query, qkv, True, False, False, heads, 0, key, key, key)
+                else:
+                    scores = ew.binary_scalar_rounded(
+                        1, ob.layout_bmm(qkv, qkv, True, False, False, heads, 0, key, key, key), key ** -0.5)
+                return ob.layout_bmm(qkv, rd.softmax(scores, -1), False, True, True, heads, 2 * key, dim)
+            return attention, attn_fused_bytes()
         return (lambda: ob.channel_select(qkv, heads, 2 * key, dim)), heads * dim * tokens * 2 * 2
     if name.startswith("detection_select"):
         from oracle import selection as sel  # the stable CPU selection, timed

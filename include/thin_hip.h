@@ -339,6 +339,27 @@ thin_status thin_channel_select_shape(const thin_desc* x, int64_t groups, int64_
 thin_status thin_channel_select(const thin_desc* x, int64_t groups, int64_t begin, int64_t count,
                                 const thin_desc* out, hipStream_t stream);
 
+/* Fused blocked attention of one C2PSA block, from the head-grouped QKV
+ * tensor to the mixed values, in one launch.  It has no single counterpart in
+ * the reference: it replaces the chain that attention_forward runs
+ * (whole_blocked.py:91-103) through channel_select, the scalar mul,
+ * layout_bmm (bmm_flow.cpp:35-191), the row softmax (softmax.cpp:6-173) and
+ * layout_bmm again, and returns that chain's bits:
+ *   prescale != 0:  s = layout_bmm(channel_select(qkv, heads, 0, key_dim) * scale,
+ *                                  qkv, T, F, F, heads, 0, key_dim, key_dim, key_dim)
+ *   prescale == 0:  s = layout_bmm(qkv, qkv, T, F, F, heads, 0, key_dim, key_dim, key_dim) * scale
+ *   out = layout_bmm(qkv, softmax(s, -1), F, T, T, heads, 2 * key_dim, head_dim)
+ * qkv: fp16 [1, C1, T, 16] with heads equal channel groups (q, k, v at
+ * offsets 0, key_dim, 2 * key_dim of each); out: fp16 [1, heads * head_dim /
+ * 16, T, 16].  `scale` multiplies in fp32 as the chain's mul does (pass the
+ * fp16-rounded scalar for the reference's 0-d operand rule).  Covered: packed
+ * 16-channel blocks (token stride 16) with a 16-byte aligned qkv, key_dim 16,
+ * 32 or 64, head_dim a multiple of 16 up to 128, T a multiple of 8 in (128,
+ * 512] with T * head_dim * 2 bytes of v fitting the kernel's LDS; other
+ * shapes return THIN_ERR_UNSUPPORTED (run the chain op by op). */
+thin_status thin_attention(const thin_desc* qkv, int64_t heads, int64_t key_dim, int64_t head_dim, float scale,
+                           int32_t prescale, const thin_desc* out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -723,6 +723,32 @@ def test_layout_bmm_and_channel_select_capture(npu):
             ops.bmm(a.unsqueeze(0), b)
 
 
+@pytest.mark.parametrize("prescale", [True, False])
+@pytest.mark.parametrize("tokens", [400, 100])
+def test_fused_attention_op(npu, prescale, tokens):
+    """thin_native_flow.attention against the op chain of whole_blocked.py:91-103
+    run op by op on the device, both orders of the scale: bit-equal.  400
+    tokens run the fused kernel; 100 (not a multiple of 8) the chain itself,
+    inside the op."""
+    ops = torch.ops.thin_native_flow
+    heads, key, dim = 4, 32, 64
+    scale = key ** -0.5
+    qkv_cpu = normal16((1, heads * (2 * key + dim) // 16, tokens, 16), 613 + tokens)
+    with torch.inference_mode():
+        qkv = qkv_cpu.to(npu)
+        got = ops.attention(qkv, heads, key, dim, scale, prescale)
+        if prescale:
+            query = ops.channel_select(qkv, heads, 0, key) * scale
+            scores = ops.layout_bmm(query, qkv, True, False, False, heads, 0, key, key, key)
+        else:
+            scores = ops.layout_bmm(qkv, qkv, True, False, False, heads, 0, key, key, key) * scale
+        expect = ops.layout_bmm(qkv, scores.softmax(dim=-1), False, True, True, heads, 2 * key, dim)
+    assert got.device.type == "npu" and got.shape == (1, heads * dim // 16, tokens, 16)
+    assert bits_equal(got.cpu(), expect.cpu())
+    with pytest.raises(RuntimeError, match="C0-aligned"):
+        ops.attention(qkv, heads, key, 2, scale, prescale)
+
+
 def test_attention_block_flow(npu):
     """The blocked attention forward of whole_blocked.py:91-110 (Q-prescaled
     order) on the device: channel_select, scale, grouped q^T k, row softmax,

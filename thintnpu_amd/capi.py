@@ -102,6 +102,7 @@ def lib() -> ctypes.CDLL:
             "thin_layout_bmm": [P, P, ctypes.POINTER(ThinBmmLayout), P, vp],
             "thin_channel_select_shape": [P, i64, i64, i64, ctypes.POINTER(i64)],
             "thin_channel_select": [P, i64, i64, i64, P, vp],
+            "thin_attention": [P, i64, i64, i64, ctypes.c_float, i32, P, vp],
         }
         for name, argtypes in sigs.items():
             fn = getattr(L, name, None)
@@ -403,4 +404,20 @@ def channel_select(x, groups: int, begin: int, count: int, out=None, stream=None
     _call("thin_channel_select_shape", _ref(desc(x)), groups, begin, count, sizes)
     out = torch.empty(tuple(sizes), dtype=torch.float16, device=x.device) if out is None else out
     _call("thin_channel_select", _ref(desc(x)), groups, begin, count, _ref(desc(out)), _stream(stream))
+    return out
+
+
+def attention(qkv, heads: int, key_dim: int, head_dim: int, scale: float, prescale: bool = True, out=None,
+              stream=None):
+    """Fused blocked attention of a head-grouped [1, C1, T, 16] QKV tensor:
+    mixed values [1, heads * head_dim / 16, T, 16], the bits of
+    channel_select -> mul -> layout_bmm -> softmax -> layout_bmm (prescale) or
+    layout_bmm -> mul -> softmax -> layout_bmm.  `scale` multiplies in fp32;
+    pass the fp16-rounded value for the reference's 0-d operand rule.  Shapes
+    outside the fused kernel's range raise ThinError (THIN_ERR_UNSUPPORTED)."""
+    tokens = qkv.shape[2]
+    if out is None:
+        out = torch.empty((1, heads * head_dim // 16, tokens, 16), dtype=torch.float16, device=qkv.device)
+    _call("thin_attention", _ref(desc(qkv)), heads, key_dim, head_dim, float(scale), int(bool(prescale)),
+          _ref(desc(out)), _stream(stream))
     return out

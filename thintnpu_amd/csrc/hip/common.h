@@ -100,6 +100,14 @@ constexpr int64_t kStreamingBytes = (int64_t)4 << 20;
 uint32_t grid_for(uint64_t units, uint32_t threads, uint32_t per_thread = 1,
                   uint32_t max_blocks = 256u * 16u);
 
+// Reduction tree of the fp16/fp32 row softmax: `lanes` lanes share a row and
+// lane g holds chunks g, g + lanes, ... (`chunks_per_lane` of them).  The row
+// sum is each lane's chunks in order, then an xor butterfly over the lanes.
+struct RowTree {
+  int lanes, chunks_per_lane;
+};
+RowTree row_tree(int64_t chunks, uint64_t rows);
+
 }  // namespace thin
 
 // ---------------------------------------------------------------- device
@@ -235,6 +243,71 @@ __device__ __forceinline__ float wave_max_nan(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max_nan(v, __shfl_xor(v, o, 64));
   return v;
+}
+
+
+// fp32 -> fp16 of the fp32 value as computed.  Without the register barrier
+// the compiler folds a producing fma or mul into v_fma_mixlo_f16, which
+// rounds the exact result to fp16 once (and forms a product as fma(a, b, +0),
+// turning -0 into +0), instead of rounding to fp32 first as the source says.
+__device__ __forceinline__ _Float16 to_half(float x) {
+  asm("" : "+v"(x));
+  return (_Float16)x;
+}
+
+// Max / sum over the G lanes of a row group (G a power of two <= 64): an xor
+// butterfly, so every lane of the group ends with the same bits.  fmaxf drops
+// a NaN operand; the row softmax relies on the sum, not the max, to carry
+// NaN through.
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, G));
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, G);
+  return v;
+}
+
+// fp16 row softmax over a row held by G lanes, KPT chunks of eight elements
+// per lane (lane g holds chunks g, g + G, ...; `have[k]` says chunk k exists):
+// m = max, e = exp2(x * log2e - m * log2e) as one fma, s = the lane's e in
+// order then the group butterfly, out = fp16(e * (1 / s)).  Shared by the row
+// softmax kernel and the fused attention kernel so both give the same bits.
+template <int G, int KPT>
+__device__ __forceinline__ void softmax_row_h8(const h8 (&x)[KPT], const bool (&have)[KPT], h8 (&out)[KPT]) {
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int k = 0; k < KPT; ++k)
+    if (have[k]) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, (float)x[k][j]);
+    }
+  m = group_max<G>(m);
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float ml = m * kLog2e;
+  float e[KPT][8];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k)
+    if (have[k]) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        e[k][j] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)x[k][j], kLog2e, -ml));
+        s += e[k][j];
+      }
+    }
+  s = group_sum<G>(s);
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int k = 0; k < KPT; ++k)
+    if (have[k]) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) out[k][j] = to_half(e[k][j] * inv);
+    }
 }
 
 }  // namespace dev

@@ -797,10 +797,16 @@ __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
   }
 }
 
-// Launches sppf_kernel for x [N,C1,H,W,16] (validated by the caller; lds =
-// the per-block LDS bytes, within kSppfLdsBytes): out = cat of x and `repeats`
-// chained pools, or with pool_only the single pool.
-thin_status launch_sppf(const thin_desc* x, int32_t kernel, int32_t repeats, bool pool_only, size_t lds,
+// Per-block LDS bytes of sppf_kernel: the padded plane and the horizontal
+// maxima, vpp 16-byte vectors per pixel.
+uint64_t sppf_lds_bytes(int64_t H, int64_t W, int R, int64_t vpp) {
+  return (uint64_t)(H + 2 * R) * (uint64_t)((W + 2 * R) + W) * (uint64_t)vpp * 16u;
+}
+
+// Launches sppf_kernel for x [N,C1,H,W,16] (validated by the caller, whose
+// plane fits kSppfLdsBytes with two vectors per pixel): out = cat of x and
+// `repeats` chained pools, or with pool_only the single pool.
+thin_status launch_sppf(const thin_desc* x, int32_t kernel, int32_t repeats, bool pool_only,
                         const thin_desc* out, hipStream_t stream) {
   const int64_t N = x->sizes[0], C1 = x->sizes[1], H = x->sizes[2], W = x->sizes[3];
   const int R = kernel / 2;
@@ -822,6 +828,7 @@ thin_status launch_sppf(const thin_desc* x, int32_t kernel, int32_t repeats, boo
   // ([1,256,20,20] k5 x3 + cat: see the SPPF row of the kernel notes)
   const bool split = N * C1 < 256;
   const int64_t vpp = split ? 1 : 2;
+  const size_t lds = (size_t)sppf_lds_bytes(H, W, R, vpp);  // the split form holds half the vectors
   p.div_row = FastDiv::make((uint32_t)(W * vpp));
   p.div_prow = FastDiv::make((uint32_t)((W + 2 * R) * vpp));
   const bool nt = numel(out) * 2 >= kStreamingBytes;
@@ -1227,10 +1234,9 @@ extern "C" thin_status thin_maxpool_nc1hwc0(const thin_desc* x, int32_t kernel, 
     // planes that fit one block's LDS: the whole-plane kernel with one pool
     // (SPPF k5 [32,256,20,20]: 5.2 us, against 7.5 us with row bands)
     const int R = kernel / 2;
-    const uint64_t lds =
-        (uint64_t)(x->sizes[2] + 2 * R) * (uint64_t)((x->sizes[3] + 2 * R) * 2 + x->sizes[3] * 2) * 16;
-    if (lds <= kSppfLdsBytes && x->sizes[0] * x->sizes[1] < ((int64_t)1 << 31))
-      return launch_sppf(x, kernel, 1, true, (size_t)lds, out, stream);
+    if (sppf_lds_bytes(x->sizes[2], x->sizes[3], R, 2) <= kSppfLdsBytes &&
+        x->sizes[0] * x->sizes[1] < ((int64_t)1 << 31))
+      return launch_sppf(x, kernel, 1, true, out, stream);
   }
   PoolPlan p;
   memset(&p, 0, sizeof p);
@@ -1268,8 +1274,7 @@ extern "C" thin_status thin_sppf_nc1hwc0(const thin_desc* x, int32_t kernel, int
                  "sppf needs 16-byte aligned pixels (C0 dense, W stride 16)");
   THIN_REQUIRE(H < (1 << 30) && W < (1 << 30), THIN_ERR_UNSUPPORTED, "sppf: plane too large");
   const int R = kernel / 2;
-  const uint64_t lds = (uint64_t)(H + 2 * R) * (uint64_t)((W + 2 * R) * 2 + W * 2) * 16;
-  if (lds > kSppfLdsBytes || N * C1 >= ((int64_t)1 << 31)) {
+  if (sppf_lds_bytes(H, W, R, 2) > kSppfLdsBytes || N * C1 >= ((int64_t)1 << 31)) {
     // planes beyond one block's LDS: the copy and the chained pools, each
     // reading the previous output slot
     auto slot = [&](int r) {
@@ -1288,7 +1293,7 @@ extern "C" thin_status thin_sppf_nc1hwc0(const thin_desc* x, int32_t kernel, int
     }
     return THIN_OK;
   }
-  return launch_sppf(x, kernel, repeats, false, (size_t)lds, out, stream);
+  return launch_sppf(x, kernel, repeats, false, out, stream);
 }
 
 extern "C" thin_status thin_maxpool2d_nchw(const thin_desc* x, int32_t kernel, const thin_desc* out,

@@ -80,18 +80,8 @@ __device__ __forceinline__ void col_offsets(const SoftmaxPlan& p, uint32_t e, in
 // so every output NaN, exactly as on CPU.  FAST (fp16 output): e = exp2(x *
 // log2e - m * log2e) as one fma; an error in the common term scales every e
 // alike and cancels in e / sum.
-template <int G>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, G));
-  return v;
-}
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, G);
-  return v;
-}
+using dev::group_max;
+using dev::group_sum;
 
 template <typename TI, typename TO, bool VEC, int G, int KPT, bool FAST, bool NT>
 __global__ __launch_bounds__(kThreads) void softmax_row_kernel(SoftmaxPlan p) {
@@ -106,6 +96,33 @@ __global__ __launch_bounds__(kThreads) void softmax_row_kernel(SoftmaxPlan p) {
   const TI* xr = static_cast<const TI*>(p.x) + xo;
   TO* orow = static_cast<TO*>(p.out) + oo;
   const uint32_t chunks = VEC ? p.R / VE : p.R;
+  if constexpr (VEC && FAST && sizeof(TI) == 2 && sizeof(TO) == 2) {
+    // fp16 in and out: the shared fp16 row core (the fused attention kernel
+    // runs the same one)
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    dev::h8 raw[KPT], out[KPT];
+    bool have[KPT];
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
+      const uint32_t c = g + G * k;
+      have[k] = live && c < chunks;
+      if (have[k]) {
+        const u4* src = reinterpret_cast<const u4*>(xr) + c;
+        raw[k] = __builtin_bit_cast(dev::h8, NT ? __builtin_nontemporal_load(src) : *src);
+      }
+    }
+    dev::softmax_row_h8<G, KPT>(raw, have, out);
+#pragma unroll
+    for (int k = 0; k < KPT; ++k) {
+      if (have[k]) {
+        u4* dst = reinterpret_cast<u4*>(orow) + (g + G * k);
+        const u4 w = __builtin_bit_cast(u4, out[k]);
+        if constexpr (NT) __builtin_nontemporal_store(w, dst);
+        else *dst = w;
+      }
+    }
+    return;
+  }
   struct alignas(VE * sizeof(TI)) WI { TI e[VE]; };
   WI raw[KPT];
   float m = -__builtin_inff();
@@ -644,22 +661,45 @@ void column_space(const thin_desc* x, const thin_desc* out, int dim, SoftmaxPlan
 // Streaming (non-temporal) loads and stores for launches moving at least
 // kStreamingBytes.
 
-// Lanes per row G and chunks per lane KPT for a row of `chunks` (<= 512).
+}  // namespace
+
+// Lanes per row G and chunks per lane KPT of the row kernel for `rows` rows of
+// `chunks` (<= 512) chunks each.  The fused attention kernel takes its softmax
+// tree from here too, so both give the same bits.
+RowTree row_tree(int64_t chunks, uint64_t rows) {
+  auto blocks = [&](int g) { return (rows + (uint64_t)kWaves * (64 / g) - 1) / ((uint64_t)kWaves * (64 / g)); };
+  if (chunks <= 2) return {1, 2};
+  if (chunks <= 4) return {2, 2};
+  if (chunks <= 8) return {4, 2};
+  if (chunks <= 16) return {8, 2};
+  if (chunks <= 32) return {16, 2};
+  if (chunks <= 64 && blocks(32) < 256) return {64, 1};  // few rows: one row per wave, more waves
+  if (chunks <= 64) return {32, 2};
+  if (chunks <= 128) return {64, 2};
+  if (chunks <= 256) return {64, 4};
+  return {64, 8};
+}
+
+namespace {
+
 template <typename TI, typename TO, bool VEC, bool FAST, bool NT>
 void launch_rows(const SoftmaxPlan& p, int64_t chunks, uint64_t rows, hipStream_t stream) {
   auto grid = [&](int g) { return (uint32_t)((rows + (uint64_t)kWaves * (64 / g) - 1) / ((uint64_t)kWaves * (64 / g))); };
 #define THIN_ROWG(G, K) hipLaunchKernelGGL((softmax_row_kernel<TI, TO, VEC, G, K, FAST, NT>), dim3(grid(G)), \
                                            dim3(kThreads), 0, stream, p)
-  if (chunks <= 2) THIN_ROWG(1, 2);
-  else if (chunks <= 4) THIN_ROWG(2, 2);
-  else if (chunks <= 8) THIN_ROWG(4, 2);
-  else if (chunks <= 16) THIN_ROWG(8, 2);
-  else if (chunks <= 32) THIN_ROWG(16, 2);
-  else if (chunks <= 64 && grid(32) < 256) THIN_ROWG(64, 1);  // few rows: one row per wave, more waves
-  else if (chunks <= 64) THIN_ROWG(32, 2);
-  else if (chunks <= 128) THIN_ROWG(64, 2);
-  else if (chunks <= 256) THIN_ROWG(64, 4);
-  else THIN_ROWG(64, 8);
+  const RowTree t = row_tree(chunks, rows);
+  switch (t.lanes * 16 + t.chunks_per_lane) {
+    case 1 * 16 + 2: THIN_ROWG(1, 2); break;
+    case 2 * 16 + 2: THIN_ROWG(2, 2); break;
+    case 4 * 16 + 2: THIN_ROWG(4, 2); break;
+    case 8 * 16 + 2: THIN_ROWG(8, 2); break;
+    case 16 * 16 + 2: THIN_ROWG(16, 2); break;
+    case 64 * 16 + 1: THIN_ROWG(64, 1); break;
+    case 32 * 16 + 2: THIN_ROWG(32, 2); break;
+    case 64 * 16 + 2: THIN_ROWG(64, 2); break;
+    case 64 * 16 + 4: THIN_ROWG(64, 4); break;
+    default: THIN_ROWG(64, 8); break;
+  }
 #undef THIN_ROWG
 }
 

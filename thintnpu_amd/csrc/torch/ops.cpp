@@ -34,20 +34,7 @@ bool float_type(const at::Tensor& t) { return t.scalar_type() == at::kFloat || t
 // ------------------------------------------------------------------ binary
 // ops.cpp:464-497.  A 0-d CPU operand is converted to the tensor's dtype
 // first, as the reference converts it (ops.cpp:466-467), so x * (1/sqrt(32))
-// multiplies by the fp16 value of 1/sqrt(32) for every op.
-// THIN_SCALAR_OPMATH=1 keeps PyTorch CPU's rule instead: the scalar rounded to
-// the tensor dtype for add/sub, held at fp32 for mul/div.
-bool scalar_opmath() {
-  static const bool on = [] {
-    const char* v = std::getenv("THIN_SCALAR_OPMATH");
-    return v && std::string(v) == "1";
-  }();
-  return on;
-}
-
-double scalar_operand(const at::Tensor& s, at::ScalarType dtype) {
-  return scalar_opmath() ? s.item<double>() : s.to(dtype).item<double>();
-}
+// multiplies by the fp16 value of 1/sqrt(32) for every op (scalar_operand).
 
 at::Tensor binary(const at::Tensor& input, const at::Tensor& other, int op, const at::Scalar& alpha = 1) {
   const bool x_scalar = input.is_cpu() && input.dim() == 0;

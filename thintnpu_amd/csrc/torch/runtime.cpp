@@ -31,6 +31,7 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <string>
 #include <thread>
 #include <unordered_map>
 #include <vector>
@@ -352,6 +353,14 @@ at::Tensor empty_bytes(int64_t bytes) {
 // ------------------------------------------------------------------ copy_
 // aten::copy_ (ops.cpp:32-78): device<->device through the strided bit-copy
 // kernel, host<->device through hipMemcpyAsync of dense staging buffers.
+double scalar_operand(const at::Tensor& s, at::ScalarType dtype) {
+  static const bool opmath = [] {
+    const char* v = std::getenv("THIN_SCALAR_OPMATH");
+    return v && std::string(v) == "1";
+  }();
+  return opmath ? s.item<double>() : s.to(dtype).item<double>();
+}
+
 at::Tensor& copy_(at::Tensor& dst, const at::Tensor& src_in, bool non_blocking) {
   (void)non_blocking;
   TORCH_CHECK(dst.scalar_type() == src_in.scalar_type(), "copy requires matching sizes and dtype");

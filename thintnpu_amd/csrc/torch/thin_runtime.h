@@ -48,4 +48,10 @@ at::Tensor empty_bytes(int64_t bytes);
 
 at::Tensor& copy_(at::Tensor& dst, const at::Tensor& src, bool non_blocking);
 
+// The value a 0-d CPU operand `s` takes in a binary op on a `dtype` tensor:
+// converted to dtype first, as the reference converts it (ops.cpp:466-467).
+// THIN_SCALAR_OPMATH=1 returns it unrounded instead; thin_binary_scalar then
+// applies PyTorch CPU's rule (rounded to dtype for add/sub, fp32 for mul/div).
+double scalar_operand(const at::Tensor& s, at::ScalarType dtype);
+
 }  // namespace thin_rt
