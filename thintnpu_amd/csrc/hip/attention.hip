@@ -13,18 +13,19 @@
 // (dev::softmax_row_h8) with the reduction tree row_tree() picks for the
 // [heads, T, T] scores, so the output equals the unfused chain bit for bit.
 //
-// One block of four waves per (head, BI query rows); the block's scores and
-// probabilities never leave LDS:
-//   1. v of the head is loaded into registers as 8-channel x 8-token tiles
-//      and stays in flight through 2-3; q rows go to LDS as fp32; each thread
-//      loads the k columns it owns.
-//   2. scores, BI rows x T columns: thread j owns columns j and j + 256, BI
-//      chains of Dk fmas each.
+// One block per (head, 8 query rows), G / 8 waves (G lanes per softmax row,
+// 64 / G rows per wave); the block's scores and probabilities never leave
+// LDS:
+//   1. q rows go to LDS (fp16), each thread loads the k columns it owns, and
+//      v of the head is loaded into registers as 8-channel x 8-token tiles
+//      that stay in flight through 2-3.
+//   2. scores, 8 rows x T columns: a thread owns one or two columns, 8 chains
+//      of Dk fmas each.
 //   3. softmax: G lanes per row, in place.
-//   4. the v tiles, transposed to [T/8][Dv][8], go to LDS.
+//   4. the v tiles, transposed to [T/8][Dv (+1 pad)][8], go to LDS.
 //   5. mixed values: lane c owns channel c (and c + 64), one chain of T fmas
 //      per row of its wave; v by 16-byte LDS reads per 8 steps, p by
-//      broadcast reads.
+//      broadcast reads, loaded four steps ahead.
 #include "common.h"
 
 #include <string.h>
@@ -35,10 +36,13 @@ namespace {
 using dev::h8;
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kAttnThreads = 256;
-constexpr uint32_t kAttnMaxTokens = 512;  // two score columns per thread
+// Query rows per block (4 with one row per wave measured slower at 400 tokens
+// x 4 heads: 11.0 against 8.9 us, though two blocks then share a CU).
+constexpr uint32_t kAttnRows = 8;
+constexpr uint32_t kAttnMaxTokens = 512;  // at most two score columns per thread
+constexpr uint32_t kAttnVTiles = 512;     // at most this many 8x8 v tiles per head
 constexpr uint32_t kAttnMaxLds = 64u * 1024u;
-constexpr uint32_t kAttnVRounds = 2;  // v tiles per thread
+constexpr uint32_t kAttnStepsPerChunk = 4;  // 8-token steps of v p^T per LDS round (one row, one channel group)
 
 struct AttnPlan {
   const _Float16* x;  // qkv [1, C1, T, 16]: token stride 16, in-block stride 1
@@ -51,16 +55,22 @@ struct AttnPlan {
   uint32_t s_off, v_off;  // byte offsets of the score and v regions in LDS (q rows at 0)
 };
 
+// G lanes per softmax row, so 64 / G rows per wave and G / 8 waves per block
+// of kAttnRows rows.
 template <int DK, int G, int KPT, int CG>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnPlan p) {
+__global__ __launch_bounds__(kAttnRows * G) void attention_kernel(AttnPlan p) {
   constexpr int RW = 64 / G;  // rows per wave
-  constexpr int BI = 4 * RW;  // rows per block
+  constexpr int BI = (int)kAttnRows;
+  constexpr uint32_t NT = kAttnRows * G;       // threads
+  constexpr uint32_t VR = kAttnVTiles / NT;     // v tiles per thread
+  constexpr uint32_t NCOL = kAttnMaxTokens / NT < 2 ? 1 : 2;  // score columns per thread
+  constexpr uint32_t PF = RW * CG >= (int)kAttnStepsPerChunk ? 1u : kAttnStepsPerChunk / (RW * CG);
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-  float* Qs = reinterpret_cast<float*>(lds);                      // [BI][DK]
+  _Float16* Qs = reinterpret_cast<_Float16*>(lds);               // [BI][DK]
   _Float16* Ss = reinterpret_cast<_Float16*>(lds + p.s_off);     // [BI][T]
-  h8* Vt = reinterpret_cast<h8*>(lds + p.v_off);                  // [T / 8][Dv]
+  h8* Vt = reinterpret_cast<h8*>(lds + p.v_off);                  // [T / 8][Dv + 1]
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t T = p.T, Dv = p.Dv;
+  const uint32_t T = p.T, Dv = p.Dv, vpitch = Dv + 1u;  // the pad vector spreads v's LDS writes over the banks
 
   // blocks of one head on one XCD (dispatch deals blocks round-robin over 8)
   uint32_t b = blockIdx.x;
@@ -69,34 +79,21 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnPlan p) {
   const uint32_t i0 = (b - h * p.row_blocks) * BI;
   const uint32_t ch0 = h * p.group;  // first channel of the head group (a multiple of 16)
 
-  // 1. v tiles into registers (consumed in step 4)
-  const uint32_t vcols = Dv / 8u, vtiles = vcols * (T / 8u);
-  h8 vraw[kAttnVRounds][8];
+  // 1. every load in flight at once: q values, the thread's k columns
+  //    j = tid + r * NT, then the v tiles (8 channels x 8 tokens), which stay
+  //    in registers until the scores and the softmax are done
+  constexpr uint32_t QR = (BI * DK + NT - 1) / NT;  // q values per thread
+  _Float16 qraw[QR];
 #pragma unroll
-  for (uint32_t r = 0; r < kAttnVRounds; ++r) {
-    const uint32_t e = tid + r * kAttnThreads;
-    if (e < vtiles) {
-      const uint32_t tg = e / vcols, c = ch0 + 2u * DK + (e - tg * vcols) * 8u;
-      const _Float16* src = p.x + (int64_t)(c >> 4) * p.xs1 + (c & 15u) + (int64_t)tg * 128;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) vraw[r][u] = *reinterpret_cast<const h8*>(src + u * 16);
-    }
+  for (uint32_t r = 0; r < QR; ++r) {
+    const uint32_t e = tid + r * NT, i = e / DK, c = e % DK, t = min(i0 + i, T - 1);
+    qraw[r] = e < (uint32_t)(BI * DK) ? p.x[(int64_t)((ch0 + c) >> 4) * p.xs1 + (int64_t)t * 16 + (c & 15u)]
+                                      : (_Float16)0.f;
   }
-  // q rows (prescaled as the unfused chain's mul rounds them) into LDS
-  for (uint32_t e = tid; e < (uint32_t)(BI * DK); e += kAttnThreads) {
-    const uint32_t i = e / DK, c = e % DK, t = i0 + i;
-    float q = 0.f;
-    if (t < T) {
-      const _Float16 raw = p.x[(int64_t)((ch0 + c) >> 4) * p.xs1 + (int64_t)t * 16 + (c & 15u)];
-      q = p.prescale ? (float)dev::to_half((float)raw * p.scale) : (float)raw;
-    }
-    Qs[e] = q;
-  }
-  // k columns j = tid, tid + 256 into registers
-  h8 kc[2][DK / 8];
+  h8 kc[NCOL][DK / 8];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const uint32_t j = min(tid + r * kAttnThreads, T - 1);
+  for (uint32_t r = 0; r < NCOL; ++r) {
+    const uint32_t j = min(tid + r * NT, T - 1);
 #pragma unroll
     for (int kb = 0; kb < DK / 16; ++kb) {
       const _Float16* src = p.x + (int64_t)((ch0 + DK) / 16u + kb) * p.xs1 + (int64_t)j * 16;
@@ -104,33 +101,80 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnPlan p) {
       kc[r][2 * kb + 1] = *reinterpret_cast<const h8*>(src + 8);
     }
   }
+  const uint32_t vcols = Dv / 8u, vtiles = vcols * (T / 8u);
+  h8 vraw[VR][8];
+#pragma unroll
+  for (uint32_t r = 0; r < VR; ++r) {
+    const uint32_t e = tid + r * NT;
+    if (e < vtiles) {
+      const uint32_t tg = e / vcols, c = ch0 + 2u * DK + (e - tg * vcols) * 8u;
+      const _Float16* src = p.x + (int64_t)(c >> 4) * p.xs1 + (c & 15u) + (int64_t)tg * 128;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vraw[r][u] = *reinterpret_cast<const h8*>(src + u * 16);
+    }
+  }
+  // q rows into LDS, prescaled as the unfused chain's mul rounds them (fp16
+  // values either way)
+#pragma unroll
+  for (uint32_t r = 0; r < QR; ++r) {
+    const uint32_t e = tid + r * NT;
+    if (e < (uint32_t)(BI * DK)) Qs[e] = p.prescale ? dev::to_half((float)qraw[r] * p.scale) : qraw[r];
+  }
   __syncthreads();
 
-  // 2. scores: per row, the sequential chain over the key channels
+  // 2. scores of the thread's columns: per row, the sequential chain over the
+  //    key channels.  The q values of channel group c8 + 1 are read while
+  //    group c8's fmas run (the compiler barriers keep it from hoisting every
+  //    q read of the loop, which would exhaust the registers).
+  {
+    float acc[NCOL][BI];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const uint32_t j = tid + r * kAttnThreads;
-    if (j < T) {
-      float acc[BI];
+    for (uint32_t r = 0; r < NCOL; ++r)
 #pragma unroll
-      for (int i = 0; i < BI; ++i) acc[i] = 0.f;
+      for (int i = 0; i < BI; ++i) acc[r][i] = 0.f;
+    h8 qa[BI], qb[BI];
+    auto read_q = [&](h8 (&q)[BI], int c8) {
 #pragma unroll
-      for (int c4 = 0; c4 < DK / 4; ++c4) {
+      for (int i = 0; i < BI; ++i) q[i] = *reinterpret_cast<const h8*>(&Qs[i * DK + 8 * c8]);
+    };
+    auto fmas = [&](const h8 (&q)[BI], int c8) {
 #pragma unroll
-        for (int i = 0; i < BI; ++i) {
-          const f4 q = *reinterpret_cast<const f4*>(&Qs[i * DK + 4 * c4]);
+      for (int u = 0; u < 8; ++u) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int c = 4 * c4 + u;
-            acc[i] = __builtin_fmaf(q[u], (float)kc[r][c / 8][c % 8], acc[i]);
-          }
+        for (uint32_t r = 0; r < NCOL; ++r) {
+          const float k = (float)kc[r][c8][u];
+#pragma unroll
+          for (int i = 0; i < BI; ++i) acc[r][i] = __builtin_fmaf((float)q[i][u], k, acc[r][i]);
         }
       }
+    };
+    // pins the chains' values here: the fmas before, the next q reads after
+    auto fence = [&]() {
 #pragma unroll
-      for (int i = 0; i < BI; ++i) {
-        _Float16 s = dev::to_half(acc[i]);
-        if (!p.prescale) s = dev::to_half((float)s * p.scale);
-        Ss[i * T + j] = s;
+      for (uint32_t r = 0; r < NCOL; ++r)
+#pragma unroll
+        for (int i = 0; i < BI; ++i) asm volatile("" : "+v"(acc[r][i])::"memory");
+    };
+    read_q(qa, 0);
+#pragma unroll
+    for (int c8 = 0; c8 < DK / 8; c8 += 2) {
+      read_q(qb, c8 + 1);
+      fmas(qa, c8);
+      fence();
+      if (c8 + 2 < DK / 8) read_q(qa, c8 + 2);
+      fmas(qb, c8 + 1);
+      fence();
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < NCOL; ++r) {
+      const uint32_t j = tid + r * NT;
+      if (j < T) {
+#pragma unroll
+        for (int i = 0; i < BI; ++i) {
+          _Float16 s = dev::to_half(acc[r][i]);
+          if (!p.prescale) s = dev::to_half((float)s * p.scale);
+          Ss[i * T + j] = s;
+        }
       }
     }
   }
@@ -154,10 +198,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnPlan p) {
       if (have[k]) *reinterpret_cast<h8*>(&Ss[i * T + 8u * (g + G * k)]) = out[k];
   }
 
-  // 4. v tiles transposed into LDS: Vt[tg][c] = v[c][8 tg .. 8 tg + 7]
+  // the v tiles, transposed to Vt[tg][c] = v[c][8 tg .. 8 tg + 7], into LDS
 #pragma unroll
-  for (uint32_t r = 0; r < kAttnVRounds; ++r) {
-    const uint32_t e = tid + r * kAttnThreads;
+  for (uint32_t r = 0; r < VR; ++r) {
+    const uint32_t e = tid + r * NT;
     if (e < vtiles) {
       const uint32_t tg = e / vcols, c = (e - tg * vcols) * 8u;
 #pragma unroll
@@ -165,13 +209,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnPlan p) {
         h8 o;
 #pragma unroll
         for (int u = 0; u < 8; ++u) o[u] = vraw[r][u][k];
-        Vt[tg * Dv + c + k] = o;
+        Vt[tg * vpitch + c + k] = o;
       }
     }
   }
   __syncthreads();
 
-  // 5. mixed values: the sequential chain over the tokens
+  // 4. mixed values: the sequential chain over the tokens.  v and p are read
+  //    from LDS PF steps at a time, the next chunk while the current one is
+  //    consumed.
   float acc[CG][RW];
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg)
@@ -181,20 +227,51 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnPlan p) {
 #pragma unroll
   for (int cg = 0; cg < CG; ++cg) cl[cg] = min(lane + 64u * cg, Dv - 1u);
   const _Float16* prow = Ss + wave * RW * T;
-#pragma unroll 2
-  for (uint32_t tg = 0; tg < T / 8u; ++tg) {
-    h8 v[CG], pv[RW];
+  const uint32_t steps = T / 8u;
+  struct Chunk {
+    h8 v[PF][CG], p[PF][RW];
+  };
+  auto load = [&](Chunk& ch, uint32_t tg0) {
 #pragma unroll
-    for (int cg = 0; cg < CG; ++cg) v[cg] = Vt[tg * Dv + cl[cg]];
+    for (uint32_t s = 0; s < PF; ++s) {
+      const uint32_t tg = min(tg0 + s, steps - 1u);  // steps past the end re-read the last (not consumed)
 #pragma unroll
-    for (int rr = 0; rr < RW; ++rr) pv[rr] = *reinterpret_cast<const h8*>(prow + rr * T + 8u * tg);
+      for (int cg = 0; cg < CG; ++cg) ch.v[s][cg] = Vt[tg * vpitch + cl[cg]];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+      for (int rr = 0; rr < RW; ++rr) ch.p[s][rr] = *reinterpret_cast<const h8*>(prow + rr * T + 8u * tg);
+    }
+  };
+  auto consume = [&](const Chunk& ch, uint32_t count) {
 #pragma unroll
-      for (int rr = 0; rr < RW; ++rr)
+    for (uint32_t s = 0; s < PF; ++s) {
+      if (s < count) {
 #pragma unroll
-        for (int cg = 0; cg < CG; ++cg)
-          acc[cg][rr] = __builtin_fmaf((float)v[cg][u], (float)pv[rr][u], acc[cg][rr]);
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int rr = 0; rr < RW; ++rr)
+#pragma unroll
+            for (int cg = 0; cg < CG; ++cg)
+              acc[cg][rr] = __builtin_fmaf((float)ch.v[s][cg][u], (float)ch.p[s][rr][u], acc[cg][rr]);
+      }
+    }
+  };
+  Chunk ca, cb;
+  load(ca, 0);
+  for (uint32_t tg0 = 0;;) {
+    if (tg0 + PF >= steps) {
+      consume(ca, steps - tg0);
+      break;
+    }
+    load(cb, tg0 + PF);
+    consume(ca, PF);
+    tg0 += PF;
+    if (tg0 + PF >= steps) {
+      consume(cb, steps - tg0);
+      break;
+    }
+    load(ca, tg0 + PF);
+    consume(cb, PF);
+    tg0 += PF;
   }
 #pragma unroll
   for (int rr = 0; rr < RW; ++rr) {
@@ -214,9 +291,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnPlan p) {
 template <int DK, int G, int KPT>
 void launch_cg(const AttnPlan& p, uint32_t lds, hipStream_t stream) {
   if (p.Dv <= 64)
-    hipLaunchKernelGGL((attention_kernel<DK, G, KPT, 1>), dim3(p.grid), dim3(kAttnThreads), lds, stream, p);
+    hipLaunchKernelGGL((attention_kernel<DK, G, KPT, 1>), dim3(p.grid), dim3(kAttnRows * G), lds, stream, p);
   else
-    hipLaunchKernelGGL((attention_kernel<DK, G, KPT, 2>), dim3(p.grid), dim3(kAttnThreads), lds, stream, p);
+    hipLaunchKernelGGL((attention_kernel<DK, G, KPT, 2>), dim3(p.grid), dim3(kAttnRows * G), lds, stream, p);
 }
 
 template <int DK>
@@ -259,11 +336,11 @@ extern "C" thin_status thin_attention(const thin_desc* qkv, int64_t heads, int64
   THIN_REQUIRE(T % 8 == 0 && T > 128 && T <= kAttnMaxTokens && (tree.lanes == 64 || tree.lanes == 32 ||
                                                                   tree.lanes == 16),
                THIN_ERR_UNSUPPORTED, "attention: tokens must be a multiple of 8 in (128, %u]", kAttnMaxTokens);
-  const uint32_t bi = 4u * (64u / (uint32_t)tree.lanes);
-  const uint32_t q_bytes = bi * (uint32_t)key_dim * 4u, s_bytes = bi * (uint32_t)T * 2u;
-  const uint32_t v_bytes = (uint32_t)(T * head_dim * 2);
+  const uint32_t bi = kAttnRows;
+  const uint32_t q_bytes = bi * (uint32_t)key_dim * 2u, s_bytes = bi * (uint32_t)T * 2u;
+  const uint32_t v_bytes = (uint32_t)(T / 8 * (head_dim + 1) * 16);
   const uint32_t lds = q_bytes + s_bytes + v_bytes;  // each part a multiple of 16 bytes
-  THIN_REQUIRE(lds <= kAttnMaxLds && (uint64_t)(head_dim / 8) * (T / 8) <= kAttnVRounds * kAttnThreads,
+  THIN_REQUIRE(lds <= kAttnMaxLds && (uint64_t)(head_dim / 8) * (T / 8) <= kAttnVTiles,
                THIN_ERR_UNSUPPORTED, "attention: %lld tokens x %lld value channels exceed the fused kernel's LDS",
                (long long)T, (long long)head_dim);
   THIN_REQUIRE(qkv->strides[1] < ((int64_t)1 << 31) && out->strides[1] < ((int64_t)1 << 31),

@@ -259,17 +259,54 @@ __device__ __forceinline__ _Float16 to_half(float x) {
 // butterfly, so every lane of the group ends with the same bits.  fmaxf drops
 // a NaN operand; the row softmax relies on the sum, not the max, to carry
 // NaN through.
-template <int G>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, G));
-  return v;
+//
+// Lane l ^ o is fetched by DPP for o <= 8 (quad_perm for 1 and 2, row
+// rotates for 4 and 8) and by the gfx950 permlane swaps for 16 and 32: a few
+// cycles per step where a ds_bpermute shuffle costs ~150.  The pairs, and so
+// the bits, are those of __shfl_xor.
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  int r;
+  if constexpr (O == 1) {
+    r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if constexpr (O == 2) {
+    r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if constexpr (O == 4) {
+    // lane i of a row reads lane (i - n) mod 16 under row_ror:n: row_ror:4
+    // into lanes 4-7 and 12-15 (banks 1, 3), row_ror:12 into 0-3 and 8-11
+    r = __builtin_amdgcn_update_dpp(x, x, 0x124, 0xF, 0xA, false);
+    r = __builtin_amdgcn_update_dpp(r, x, 0x12C, 0xF, 0x5, false);
+  } else if constexpr (O == 8) {
+    r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (O == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+    r = (int)((threadIdx.x & 16u) ? s[0] : s[1]);
+  } else {
+    static_assert(O == 32, "lane_xor: offset must be a power of two below 64");
+    const auto s = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+    r = (int)((threadIdx.x & 32u) ? s[0] : s[1]);
+  }
+  return __builtin_bit_cast(float, r);
 }
-template <int G>
+
+template <int G, int O = G / 2>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (O == 0) {
+    return v;
+  } else {
+    v = fmaxf(v, lane_xor<O>(v));
+    return group_max<G, O / 2>(v);
+  }
+}
+template <int G, int O = G / 2>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, G);
-  return v;
+  if constexpr (O == 0) {
+    return v;
+  } else {
+    v += lane_xor<O>(v);
+    return group_sum<G, O / 2>(v);
+  }
 }
 
 // fp16 row softmax over a row held by G lanes, KPT chunks of eight elements
