@@ -225,6 +225,90 @@ def op_sigmoid(capi, dev, n, rotate=True):
     return (lambda st: capi.unary(capi.SIGMOID, st[0], out=st[1])), sets, algo
 
 
+def op_bcast_binary(capi, dev, n, c, h, w, op, narrowed, rotate=True):
+    """What aten mul / add run on the device for an NC1HWC0 [n,C1,H,W,16]
+    tensor and a per-channel [1,C1,1,1,16] operand (the unfused scale and
+    shift of a convolution's output, ops.cpp:464-497 of the reference): one
+    thin_binary launch over the broadcast view into a fresh contiguous output,
+    on the full tensor or the C2f half x[:, C1/2:]."""
+    c1 = c // 16
+    full = n * c1 * h * w * 16 * 2
+    part = full // 2 if narrowed else full
+    algo = 2 * part + (c1 // 2 if narrowed else c1) * 16 * 2
+
+    def make(i):
+        x = blocked_normal(n, c, h, w, 400 + i, dev)
+        g = torch.Generator(device=dev).manual_seed(500 + i)
+        s = (torch.rand((1, c1, 1, 1, 16), generator=g, device=dev) + 0.5).half()
+        if narrowed:
+            x, s = x[:, c1 // 2:], s[:, c1 // 2:]
+        return x, s, torch.empty(x.shape, dtype=torch.float16, device=dev)
+    sets = rotated(make, full + part, rotate)
+    return (lambda st: capi.binary(op, st[0], st[1], out=st[2])), sets, algo
+
+
+def op_c1_unary_binary(capi, dev, n, which, rotate=True):
+    """C1 as separate aten ops: SiLU of [n,64,160,160] NC1HWC0, or the add of
+    two such tensors (the residual), each one launch."""
+    per = n * 4 * 160 * 160 * 16 * 2
+    if which == "silu":
+        sets = rotated(lambda i: (blocked_normal(n, 64, 160, 160, 600 + i, dev),
+                                  torch.empty((n, 4, 160, 160, 16), dtype=torch.float16, device=dev)), per * 2, rotate)
+        return (lambda st: capi.unary(capi.SILU, st[0], out=st[1])), sets, per * 2
+    sets = rotated(lambda i: (blocked_normal(n, 64, 160, 160, 620 + i, dev), blocked_normal(n, 64, 160, 160, 640 + i, dev),
+                              torch.empty((n, 4, 160, 160, 16), dtype=torch.float16, device=dev)), per * 3, rotate)
+    return (lambda st: capi.binary(capi.ADD, st[0], st[1], out=st[2])), sets, per * 3
+
+
+C2F_CHAIN = (128, 80, 80)  # the C2f tensor the captured chain runs on
+
+
+def c2f_chain(x):
+    """The tail of a C2f block as a drop-in caller writes it: split the
+    convolution's output in two, SiLU in place on one half, the residual add,
+    and the concatenation (NC1HWC0 channel blocks, dim 1)."""
+    a, b = x.split(x.shape[1] // 2, dim=1)
+    torch.nn.functional.silu(b, inplace=True)
+    return torch.cat([a, b, a + b], dim=1)
+
+
+def c2f_chain_bytes(n):
+    c, h, w = C2F_CHAIN
+    half = n * (c // 32) * h * w * 16 * 2
+    return 11 * half  # silu_ 2, add 3, cat 6 halves
+
+
+def time_c2f_captured(n, replays, rounds=5, rotate=True):
+    """Wall-clock seconds per CapturedForward replay of c2f_chain on the npu
+    device (a HIP graph launched on the calling thread's stream; replays are
+    asynchronous, so back-to-back replays measure the device time unless the
+    graph is shorter than its host launch).  Buffers rotate over several
+    captured forwards like the other rows."""
+    import thin_backend  # noqa: F401  (the npu device)
+    from thin_backend.graph import CapturedForward
+    c, h, w = C2F_CHAIN
+    npu = torch.device("npu:0")
+    count = rotation_count(c2f_chain_bytes(n)) if rotate else 1
+    graphs = []
+    with torch.inference_mode():
+        for i in range(count):
+            x = torch.randn((n, c // 16, h, w, 16), generator=gen(700 + i)).half().to(npu)
+            graphs.append(CapturedForward(c2f_chain, x))
+        for gph in graphs:
+            gph.replay()
+        thin_backend.synchronize()
+        res = []
+        for _ in range(rounds):
+            t0 = time.perf_counter()
+            for k in range(replays):
+                graphs[k % count].replay()
+            thin_backend.synchronize()
+            res.append((time.perf_counter() - t0) / replays)
+        for gph in graphs:
+            gph.close()
+    return statistics.median(res)
+
+
 def op_softmax(capi, dev, n, rotate=True):
     """C5 attention row softmax [n,4,400,400]."""
     algo = n * 4 * 400 * 400 * 2 * 2
@@ -421,6 +505,15 @@ def op_rows(capi, dev):
                 rows.append((name, "C2", n, lambda r, n=n, c=c, h=h, w=w, nr=narrowed:
                              op_affine_silu(capi, dev, n, c, h, w, nr, r)))
     for n in (1, 32):
+        for which in ("silu", "add"):
+            rows.append((f"{which}_c1", "C1", n, lambda r, n=n, wh=which: op_c1_unary_binary(capi, dev, n, wh, r)))
+    for (c, h, w) in C2_SHAPES:
+        for opname, op in (("mul", capi.MUL), ("add", capi.ADD)):
+            for narrowed in (False, True):
+                name = f"aten_{opname}_bcast{'_narrowed' if narrowed else ''}_{c}x{h}x{w}"
+                rows.append((name, "C2", 32, lambda r, c=c, h=h, w=w, op=op, nr=narrowed:
+                             op_bcast_binary(capi, dev, 32, c, h, w, op, nr, r)))
+    for n in (1, 32):
         rows.append(("cat_c2f_4x64", "C3", n, lambda r, n=n: op_cat_c2f(capi, dev, n, r)))
         rows.append(("upsample2x_256x40x40", "C3", n, lambda r, n=n: op_upsample(capi, dev, n, r)))
         rows.append(("upsample_cat_256+128", "C3", n, lambda r, n=n: op_upsample_cat(capi, dev, n, r)))
@@ -459,6 +552,21 @@ def cpu_op(name, n):
     if name == "silu_add":
         x, y = h16(n, 4, 160, 160, 16), h16(n, 4, 160, 160, 16)
         return (lambda: y + F.silu(x)), n * 4 * 160 * 160 * 16 * 2 * 3
+    if name in ("silu_c1", "add_c1"):
+        x, y = h16(n, 4, 160, 160, 16), h16(n, 4, 160, 160, 16)
+        return ((lambda: F.silu(x)), x.numel() * 4) if name == "silu_c1" else ((lambda: x + y), x.numel() * 6)
+    if name.startswith("aten_"):
+        c, h, w = (int(v) for v in name.rsplit("_", 1)[1].split("x"))
+        c1 = c // 16
+        x, sc = h16(n, c1, h, w, 16), h16(1, c1, 1, 1, 16).abs() + 0.5
+        if "narrowed" in name:
+            x, sc = x[:, c1 // 2:], sc[:, c1 // 2:]
+        fn = (lambda: x * sc) if name.startswith("aten_mul") else (lambda: x + sc)
+        return fn, x.numel() * 4
+    if name == "c2f_chain_captured":
+        c, h, w = C2F_CHAIN
+        x = h16(n, c // 16, h, w, 16)
+        return (lambda: c2f_chain(x)), c2f_chain_bytes(n)
     if name == "pack_nc1hwc0":
         x = h16(n, 64, 160, 160)
         return (lambda: x.view(n, 4, 16, 160, 160).permute(0, 1, 3, 4, 2).contiguous()), x.numel() * 4
@@ -636,6 +744,12 @@ def main():
     capi.lib()
     dev = torch.device("cuda:0")
     n = 32
+    if args.profile and args.profile.startswith("op:c2f_chain_captured"):
+        nn = int(args.profile.partition("@")[2] or 32)
+        t = time_c2f_captured(nn, args.iters)
+        print(json.dumps({"profile": f"c2f_chain_captured N={nn}", "us": round(t * 1e6, 3),
+                          "GB/s": round(c2f_chain_bytes(nn) / t / 1e9, 1), "bytes": c2f_chain_bytes(nn)}))
+        return
     if args.profile and args.profile.startswith("op:"):
         name, _, nn = args.profile[3:].partition("@")
         rows = [(rn, f) for (rname, _, rn, f) in op_rows(capi, dev) if rname == name]
@@ -767,6 +881,31 @@ def main():
                     (f"   cpu {cpu_row['cpu_us']:10.1f} us  1 thread {cpu_row['cpu1_us']:10.1f} us"
                      if cpu_row else ""))
                 del sets
+                torch.cuda.empty_cache()
+
+        # the drop-in path as callers use it: a CapturedForward-replayed C2f
+        # tail on the npu device (wall clock per replay)
+        for nn in (1, 32):
+            cpu_row = None
+            if not args.no_cpu:
+                fn, cpu_bytes = cpu_op("c2f_chain_captured", nn)
+                ct, ns = time_cpu(fn)
+                cpu_row = {"cpu_us": round(ct * 1e6, 1), "cpu_GB/s": round(cpu_bytes / ct / 1e9, 2),
+                           "cpu_threads": torch.get_num_threads(), "cpu_samples": ns}
+                del fn
+            for rotate in ((False, True) if nn == 1 else (True,)):
+                t = time_c2f_captured(nn, args.iters, rotate=rotate)
+                algo = c2f_chain_bytes(nn)
+                gbs = algo / t / 1e9
+                row = {"op": "c2f_chain_captured", "cfg": "C2f", "N": nn, "us": round(t * 1e6, 3),
+                       "GB/s": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1), "bytes": algo,
+                       "cache": "rotated" if rotate else "resident",
+                       "note": "CapturedForward replay on npu (split, silu_, add, cat), wall clock per replay"}
+                if cpu_row:
+                    row.update(cpu_row)
+                ops.append(row)
+                log(f"C2f {'c2f_chain_captured':32s} N={nn:2d} {'rot' if rotate else 'res'} "
+                    f"{t * 1e6:9.2f} us {gbs:8.1f} GB/s")
                 torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline()
