@@ -104,24 +104,22 @@ def time_launches(launch, sets, iters, rounds=5):
     return statistics.median(res)
 
 
-# rocprofv3 --pmc readings (KiB per dispatch, median over the dispatches) of the
-# dominant kernel, affine_silu_flat_kernel at N=32 (128,80,80), and of the dense
-# copy map_dense_kernel<OpCopy> over the same [32,8,80,80,16] fp16 tensor
-# (104857600 B read + written), from `bench.py --profile dominant|copy --iters 20`
-# (profiles/affine_silu_flat_n32_128x80x80_pmc.md).
-PMC_KIB = {"dominant": {"FETCH_SIZE": 25622.0, "WRITE_SIZE": 51200.0},
-           "copy": {"FETCH_SIZE": 25610.0, "WRITE_SIZE": 51257.25}}
-COPY_BYTES_EACH_WAY = 52428800
+# rocprofv3 --pmc readings of the dominant kernel, affine_silu_flat_kernel at
+# N=32 (128,80,80): memory requests the L2 sent to HBM per dispatch, by size
+# (TCC_EA0_RDREQ_32B/_64B/_128B, TCC_EA0_WRREQ and TCC_EA0_WRREQ_64B, summed over
+# the L2 channels, median over 123 dispatches) from
+# `bench.py --profile dominant --iters 20` (profiles/affine_silu_flat_n32_128x80x80_pmc.md).
+# Every request is counted once at its size, so bytes = sum(size x count)
+# without any calibration; write requests that are not 64-byte are 32-byte.
+DOMINANT_REQUESTS = {"RDREQ_32B": 0, "RDREQ_64B": 320, "RDREQ_128B": 409632, "WRREQ": 819202, "WRREQ_64B": 819202}
 
 
 def dominant_traffic():
-    """HBM bytes per launch of the dominant kernel: each counter scaled by what
-    it reads for the copy of known size (FETCH_SIZE reads half the bytes a
-    16-byte-per-lane copy loads on gfx950, WRITE_SIZE the full amount)."""
-    fetch = COPY_BYTES_EACH_WAY / (PMC_KIB["copy"]["FETCH_SIZE"] * 1024)
-    write = COPY_BYTES_EACH_WAY / (PMC_KIB["copy"]["WRITE_SIZE"] * 1024)
-    d = PMC_KIB["dominant"]
-    return int(round(d["FETCH_SIZE"] * 1024 * fetch + d["WRITE_SIZE"] * 1024 * write))
+    """HBM bytes per launch of the dominant kernel from its request counters."""
+    r = DOMINANT_REQUESTS
+    read = 32 * r["RDREQ_32B"] + 64 * r["RDREQ_64B"] + 128 * r["RDREQ_128B"]
+    write = 64 * r["WRREQ_64B"] + 32 * (r["WRREQ"] - r["WRREQ_64B"])
+    return read + write
 
 
 def rotation_count(bytes_per_set):
@@ -840,8 +838,8 @@ def main():
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": dominant_traffic(),
                 "kernel": "affine_silu_flat_kernel<2, true, true> (thin_affine_silu)",
                 "launch": f"N=32 C,H,W={C2_SHAPES[0]}: {algo} algorithmic bytes, avg {dom_s * 1e6:.2f} us",
-                "traffic_note": "HBM bytes per launch = FETCH_SIZE x fetch factor + WRITE_SIZE x write factor, "
-                                "factors from a plain 16-byte copy of the same tensor (rocprofv3 --pmc, "
+                "traffic_note": "HBM bytes per launch = sum of L2-to-HBM read and write requests x their "
+                                "sizes (rocprofv3 --pmc TCC_EA0_RDREQ_32B/_64B/_128B, TCC_EA0_WRREQ/_64B; "
                                 "profiles/affine_silu_flat_n32_128x80x80_pmc.md)"}
     del sets
 
