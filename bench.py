@@ -728,8 +728,10 @@ def main():
     ap.add_argument("--iters", type=int, default=200, help="launches per per-op timing round")
     ap.add_argument("--profile", default=None,
                     help="replay one kernel only and print its timing (rocprofv3 summaries / counter "
-                         "calibration): 'dominant', 'copy' (a plain 16-byte copy of the same size), or "
-                         "'op:<row name>[@N]' for one row of the per-op table (N=32 by default, rotated)")
+                         "calibration): 'dominant', 'copy' (a plain 16-byte copy of the same size), "
+                         "'copy@<C>x<H>x<W>' (a copy of one N=32 C2 tensor), 'floor' (a one-element fill: "
+                         "the per-launch floor), or 'op:<row name>[@N]' for one row of the per-op table "
+                         "(N=32 by default, rotated)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of "
@@ -761,6 +763,23 @@ def main():
         t = time_launches(launch, sets, args.iters)
         print(json.dumps({"profile": f"{name} N={nn}", "us": round(t * 1e6, 3), "GB/s": round(algo / t / 1e9, 1),
                           "bytes": algo}))
+        return
+    if args.profile == "floor":
+        # the per-launch floor: a one-element thin_fill (one block) replayed
+        # back to back from a HIP graph like every row
+        sets = [torch.empty(1, dtype=torch.float16, device=dev) for _ in range(2)]
+        t = time_launches(lambda st: capi.fill(st, 1.0), sets, args.iters)
+        print(json.dumps({"profile": "thin_fill of one fp16 element (one block)", "us": round(t * 1e6, 3)}))
+        return
+    if args.profile and args.profile.startswith("copy@"):
+        # a plain copy of the bytes of one C2 launch: [32,C/16,H,W,16] fp16
+        c, h, w = (int(v) for v in args.profile[5:].split("x"))
+        per = n * (c // 16) * h * w * 16 * 2
+        sets = rotated(lambda i: (blocked_normal(n, c, h, w, 800 + i, dev),
+                                  torch.empty((n, c // 16, h, w, 16), dtype=torch.float16, device=dev)), 2 * per, True)
+        t = time_launches(lambda st: capi.copy(st[0], st[1]), sets, args.iters)
+        print(json.dumps({"profile": f"copy of [{n},{c // 16},{h},{w},16] fp16", "us": round(t * 1e6, 3),
+                          "GB/s": round(2 * per / t / 1e9, 1), "bytes": 2 * per}))
         return
     if args.profile:
         if args.profile not in ("dominant", "copy"):
