@@ -110,6 +110,16 @@ def assert_fused_cancel(actual: torch.Tensor, expected: torch.Tensor, term: torc
     r = expected.detach().cpu().double()
     m = torch.isfinite(r)
     err = (a - r).abs()[m]
-    ok = (err <= max_ulp * ulp16_spacing(r)[m]) | (err <= term_ulp32 * ulp32_spacing(term)[m])
+    ulp_arm = err <= max_ulp * ulp16_spacing(r)[m]
+    ok = ulp_arm | (err <= term_ulp32 * ulp32_spacing(term)[m])
     assert bool(ok.all()), f"{what}: {int((~ok).sum())} elements outside the fused bound ({rep})"
+    # elements that pass only through the cancellation arm, and how far they are
+    only = (~ulp_arm).numpy()
+    rep["cancel_only"] = int(only.sum())
+    if rep["cancel_only"]:
+        fa = ordered16(bits16(actual).reshape(-1)[m.reshape(-1).numpy()])
+        fr = ordered16(bits16(expected).reshape(-1)[m.reshape(-1).numpy()])
+        rep["cancel_max_ulp"] = int(np.abs(fa - fr)[only].max())
+    else:
+        rep["cancel_max_ulp"] = 0
     return rep

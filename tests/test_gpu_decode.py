@@ -3,13 +3,15 @@
 The fused kernel must equal, bit for bit, the composition of entries pinned
 elsewhere: thin_dfl_expect (fp16 distances) -> the oracle's fp16 box steps ->
 and thin_unary SIGMOID for the scores.  Against the full CPU oracle the boxes
-differ only through the DFL expectation's 1e-3 relative bar."""
+differ only through the DFL expectation's 1e-3 relative bar, carried through
+the box steps with one fp16 rounding per step (box_bound)."""
 import pytest
 import torch
 
 from oracle import detect as dt
 from oracle import elementwise as ew
-from oracle.numerics import assert_ulp, bits_equal
+from oracle import reductions as rd
+from oracle.numerics import assert_ulp, bits_equal, ulp16_spacing
 from tests.helpers import normal16
 
 pytestmark = pytest.mark.gpu
@@ -40,8 +42,32 @@ def test_decode_equals_composition(gpu, xywh, case):
     assert bits_equal(got, want)
     ref = dt.detect_decode(boxes, scores, shapes, strides, xywh)
     assert_ulp(got[:, 4:], ref[:, 4:], 2, "scores")
-    scale = dt.grid(shapes, strides)[1]
-    assert ((got[:, :4].float() - ref[:, :4].float()).abs() <= scale.float() * 0.05).all()
+    distance = capi.dfl_expect(boxes.to(gpu)).cpu()
+    bound = box_bound(distance, rd.dfl_expect(boxes, torch.float16), shapes, strides, xywh)
+    assert ((got[:, :4].double() - ref[:, :4].double()).abs() <= bound * (1 + 1e-9)).all()
+
+
+def box_bound(d_dev, d_ref, shapes, strides, xywh):
+    """Largest |device box - oracle box| the contracts allow.  The two
+    distances differ by at most the DFL bar (1e-3 of |d|, floored at 2^-14);
+    each fp16 box step of either path adds at most half an ulp of its
+    result; the stride multiply is exact (a power of two).  In units of the
+    output (pixels)."""
+    anchors, scale = dt.grid(shapes, strides)
+    a, st = anchors.double().unsqueeze(0), scale.double().unsqueeze(0)
+    e = 1e-3 * d_ref.double().abs().clamp_min(2.0 ** -14)
+    h = lambda t: 0.5 * ulp16_spacing(t)  # noqa: E731  (half an ulp at |t|)
+    lo = [a - d[:, :2].double() for d in (d_dev, d_ref)]
+    up = [a + d[:, 2:].double() for d in (d_dev, d_ref)]
+    r_lo = h(lo[0]) + h(lo[1])       # the rounding of each path's lower and upper
+    r_up = h(up[0]) + h(up[1])
+    if not xywh:
+        return torch.cat((e[:, :2] + r_lo, e[:, 2:] + r_up), 1) * st
+    c = [(l_ + u_) / 2 for l_, u_ in zip(lo, up)]
+    w = [u_ - l_ for l_, u_ in zip(lo, up)]
+    bc = (e[:, :2] + e[:, 2:]) / 2 + (r_lo + r_up) / 2 + h(c[0]) + h(c[1])
+    bw = e[:, :2] + e[:, 2:] + r_lo + r_up + h(w[0]) + h(w[1])
+    return torch.cat((bc, bw), 1) * st
 
 
 def test_decode_views_and_specials(gpu):
