@@ -82,13 +82,16 @@ __global__ __launch_bounds__(kAttnRows * G) void attention_kernel(AttnPlan p) {
   // 1. every load in flight at once: q values, the thread's k columns
   //    j = tid + r * NT, then the v tiles (8 channels x 8 tokens), which stay
   //    in registers until the scores and the softmax are done
+  //    Every thread issues the same loads (indexes clamped in range, surplus
+  //    values unused), so the compiler can count them: with loads under a
+  //    branch its wait counts turn conservative and the scores would wait
+  //    for the v tiles.
   constexpr uint32_t QR = (BI * DK + NT - 1) / NT;  // q values per thread
   _Float16 qraw[QR];
 #pragma unroll
   for (uint32_t r = 0; r < QR; ++r) {
-    const uint32_t e = tid + r * NT, i = e / DK, c = e % DK, t = min(i0 + i, T - 1);
-    qraw[r] = e < (uint32_t)(BI * DK) ? p.x[(int64_t)((ch0 + c) >> 4) * p.xs1 + (int64_t)t * 16 + (c & 15u)]
-                                      : (_Float16)0.f;
+    const uint32_t e = min(tid + r * NT, (uint32_t)(BI * DK) - 1u), i = e / DK, c = e % DK, t = min(i0 + i, T - 1);
+    qraw[r] = p.x[(int64_t)((ch0 + c) >> 4) * p.xs1 + (int64_t)t * 16 + (c & 15u)];
   }
   h8 kc[NCOL][DK / 8];
 #pragma unroll
@@ -101,17 +104,17 @@ __global__ __launch_bounds__(kAttnRows * G) void attention_kernel(AttnPlan p) {
       kc[r][2 * kb + 1] = *reinterpret_cast<const h8*>(src + 8);
     }
   }
+  // the q and k loads stay ahead of the v loads (their waits must not cover v)
+  asm volatile("" ::: "memory");
   const uint32_t vcols = Dv / 8u, vtiles = vcols * (T / 8u);
   h8 vraw[VR][8];
 #pragma unroll
   for (uint32_t r = 0; r < VR; ++r) {
-    const uint32_t e = tid + r * NT;
-    if (e < vtiles) {
-      const uint32_t tg = e / vcols, c = ch0 + 2u * DK + (e - tg * vcols) * 8u;
-      const _Float16* src = p.x + (int64_t)(c >> 4) * p.xs1 + (c & 15u) + (int64_t)tg * 128;
+    const uint32_t e = min(tid + r * NT, vtiles - 1u);
+    const uint32_t tg = e / vcols, c = ch0 + 2u * DK + (e - tg * vcols) * 8u;
+    const _Float16* src = p.x + (int64_t)(c >> 4) * p.xs1 + (c & 15u) + (int64_t)tg * 128;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) vraw[r][u] = *reinterpret_cast<const h8*>(src + u * 16);
-    }
+    for (int u = 0; u < 8; ++u) vraw[r][u] = *reinterpret_cast<const h8*>(src + u * 16);
   }
   // q rows into LDS, prescaled as the unfused chain's mul rounds them (fp16
   // values either way)
