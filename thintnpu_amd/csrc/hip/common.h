@@ -265,8 +265,8 @@ __device__ __forceinline__ _Float16 to_half(float x) {
 // cycles per step where a ds_bpermute shuffle costs ~150.  The pairs, and so
 // the bits, are those of __shfl_xor.
 template <int O>
-__device__ __forceinline__ float lane_xor(float v) {
-  const int x = __builtin_bit_cast(int, v);
+__device__ __forceinline__ uint32_t lane_xor_bits(uint32_t v) {
+  const int x = (int)v;
   int r;
   if constexpr (O == 1) {
     r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
@@ -287,7 +287,11 @@ __device__ __forceinline__ float lane_xor(float v) {
     const auto s = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
     r = (int)((threadIdx.x & 32u) ? s[0] : s[1]);
   }
-  return __builtin_bit_cast(float, r);
+  return (uint32_t)r;
+}
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+  return __builtin_bit_cast(float, lane_xor_bits<O>(__builtin_bit_cast(uint32_t, v)));
 }
 
 template <int G, int O = G / 2>

@@ -16,6 +16,8 @@
 // the caller's workspace with a multi-launch bitonic network.
 #include "common.h"
 
+#include <type_traits>
+
 #include <string.h>
 
 #include <algorithm>
@@ -911,16 +913,48 @@ __global__ __launch_bounds__(kSliceThreads) void slice_kernel(SplitPlan p) {
     groups = kGroups;
   }
   __syncthreads();
+  // Minimum over the class groups of each anchor.  Keys carry their class in
+  // the low bits, so every key of an anchor is distinct and any reduction
+  // order gives the same minimum (and its score bits).  The vector form's 32
+  // groups reduce in two levels with every load of a level in flight at once
+  // (a serial loop of 31 dependent LDS reads cost ~3 us per slice).
+  constexpr uint32_t kParts = kSliceThreads / kSlice;  // 4
+  __shared__ uint32_t part_kc[kParts * kSlice];
+  __shared__ uint16_t part_bits[kParts * kSlice];
+  auto reduce = [&](const uint32_t* kcs, const uint16_t* bitss, auto count, uint32_t first, uint32_t& best,
+                    uint32_t& bb) {
+    constexpr uint32_t N = decltype(count)::value;
+    uint32_t k[N], h[N];
+#pragma unroll
+    for (uint32_t g = 0; g < N; ++g) {
+      k[g] = kcs[(first + g) * kSlice];
+      h[g] = bitss[(first + g) * kSlice];
+    }
+    best = k[0];
+    bb = h[0];
+#pragma unroll
+    for (uint32_t g = 1; g < N; ++g)
+      if (k[g] < best) {
+        best = k[g];
+        bb = h[g];
+      }
+  };
+  uint32_t best = kPad, bb = 0u;
+  if (groups == kVGroups) {
+    static_assert(kVGroups == kParts * 8, "two-level group reduction");
+    const uint32_t x = tid % kSlice, q = tid / kSlice;
+    reduce(g_kc + x, g_bits + x, std::integral_constant<uint32_t, 8>(), q * 8u, best, bb);
+    part_kc[q * kSlice + x] = best;
+    part_bits[q * kSlice + x] = (uint16_t)bb;
+    __syncthreads();
+    if (tid < kSlice)
+      reduce(part_kc + tid, part_bits + tid, std::integral_constant<uint32_t, kParts>(), 0u, best, bb);
+  } else if (tid < kSlice) {
+    static_assert(kGroups == kParts, "scalar form: one group per part");
+    reduce(g_kc + tid, g_bits + tid, std::integral_constant<uint32_t, kGroups>(), 0u, best, bb);
+  }
   if (tid < kSlice) {
     const uint32_t a = slice * kSlice + tid;
-    uint32_t best = g_kc[tid], bb = g_bits[tid];
-    for (uint32_t g = 1; g < groups; ++g) {
-      const uint32_t k = g_kc[g * kSlice + tid];
-      if (k < best) {
-        best = k;
-        bb = g_bits[g * kSlice + tid];
-      }
-    }
     uint32_t rec = kPad;
     if (a < p.A) {
       const size_t t = (size_t)b * p.A + a;
@@ -1092,22 +1126,27 @@ __device__ __forceinline__ void rank_candidates(const uint32_t* lists, uint32_t 
 // All loads come before any store: a wave waits for its stores as well as its
 // loads when it needs a load result, so interleaving them would serialise on
 // store completion.
+// Row t of out (fp32 bits: box, score, label) and its trace entries.
+__device__ __forceinline__ void put_row(uint32_t* out, const thin_select_trace& tr, size_t t, const uint32_t (&box)[4],
+                                        int64_t a, int64_t label, uint32_t sbits, int64_t stage2) {
+  uint32_t* o = out + t * 6;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) o[c] = float_bits(box[c]);
+  o[4] = float_bits(sbits);
+  o[5] = __float_as_uint((float)label);
+  if (tr.stage2 && stage2 >= 0) static_cast<int64_t*>(tr.stage2)[t] = stage2;
+  if (tr.anchors) static_cast<int64_t*>(tr.anchors)[t] = a;
+  if (tr.labels) static_cast<int64_t*>(tr.labels)[t] = label;
+  if (tr.top_values) static_cast<uint16_t*>(tr.top_values)[t] = (uint16_t)sbits;
+}
+
 __device__ __forceinline__ void pack_out(const SplitPlan& p, uint32_t b, uint32_t r, int64_t a, int64_t label,
                                          uint32_t sbits, int64_t stage2) {
   const uint16_t* bx = p.L.x + b * p.L.sb + a * p.L.sa;
   uint32_t box[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) box[c] = bx[c * p.L.sc];
-  const size_t t = (size_t)b * p.K + r;
-  uint32_t* o = p.out + t * 6;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) o[c] = float_bits(box[c]);
-  o[4] = float_bits(sbits);
-  o[5] = __float_as_uint((float)label);
-  if (p.tr.stage2 && stage2 >= 0) static_cast<int64_t*>(p.tr.stage2)[t] = stage2;
-  if (p.tr.anchors) static_cast<int64_t*>(p.tr.anchors)[t] = a;
-  if (p.tr.labels) static_cast<int64_t*>(p.tr.labels)[t] = label;
-  if (p.tr.top_values) static_cast<uint16_t*>(p.tr.top_values)[t] = (uint16_t)sbits;
+  put_row(p.out, p.tr, (size_t)b * p.K + r, box, a, label, sbits, stage2);
 }
 
 __global__ __launch_bounds__(kSplitThreads) void merge1_kernel(SplitPlan p) {
@@ -1198,6 +1237,842 @@ __global__ __launch_bounds__(kSplitThreads) void merge2_kernel(SplitPlan p) {
   });
 }
 
+// ---------------------------------------------------------------- two-launch selection
+// The selection in two launches, for one image or a few:
+//
+//   runs   (grid runs x B, 512 threads): per anchor of kRun, the three
+//          smallest (key << 16 | class) over the classes; the run's
+//          (key << 16 | anchor) records sorted (a bitonic network over two
+//          waves) -> runs_rec, with each record's row key (below) ->
+//          runs_side; per anchor a 16-byte info record (box, class-max score
+//          bits and class, second key and class) -> info.
+//   finish (grid B, 1024 threads): the stage-1 candidates of the sorted runs
+//          (the prefix bound of the split kernels), sorted, while the info of
+//          every candidate and the score rows of the few candidates whose
+//          third key could reach the bound are in flight; stage 2 from the K
+//          class-max pairs, the second pairs and those rows; rows packed
+//          from LDS.
+//
+// Stage 2 is the top K of the stage-1 anchors' pairs keyed at most T1 (the K
+// class-max pairs are among them): the class-max pairs (key_r, r * nc +
+// class_r), the second pair of every anchor whose second key is at most T1,
+// and, for an anchor whose third key is at most T1, every pair of its row.
+// T1 is at most the candidate bound, so those rows are among the prefetched
+// ones.  A second pair's score bits follow from its key, except for NaN and
+// zero keys (several encodings each): rows with such a second key are
+// prefetched too.  A run record's row key is the smallest key that makes its
+// row needed: the third key, or the second key when that is NaN or zero.  When the rows do not fit (thousands of tied scores), or a
+// trace of the gathered scores is asked for, every stage-1 row is gathered
+// into an LDS table instead, and ties beyond kSortCap survivors go through a
+// radix select of the K-th smallest pair.
+//
+// Sorting in one workgroup is a bitonic network over at most kSortCap
+// records, held by four waves (E records per thread for n = 256E; smaller n a
+// record per thread): exchanges within a thread in registers, within a wave
+// by DPP and permlane swaps, between waves through LDS.  More stage-1
+// candidates than kSortCap go through an exact radix select of the K-th
+// smallest record first (four 8-bit digits, LDS histograms), so only K
+// records are sorted.  Records are unique, so the network's order is the
+// stable (key, index) order.
+constexpr uint32_t kRun = 128;             // anchors per sorted run
+constexpr uint32_t kRunThreads = 512;      // runs_kernel workgroups
+constexpr uint32_t kMaxRuns = 128;         // runs per image (A <= 16384)
+constexpr uint32_t kRunPitch = kRun + 4;   // finish LDS words per run list (run l on banks 4l mod 64)
+constexpr uint32_t kSidePitch = kRun + 8;  // finish LDS halves per run row-key list (16-byte rows)
+constexpr uint32_t kFinishThreads = 1024;  // finish_kernel workgroups
+constexpr uint32_t kSortCap = 1024;        // records one bitonic sort holds
+constexpr uint32_t kPairTable = 32768;     // K * nc limit: every stage-1 row in LDS (fallback)
+constexpr uint32_t kGatherBatch = 32;      // fallback gather: pair loads in flight per thread
+constexpr uint32_t kMaxX = 256;            // prefetched candidate rows
+constexpr uint32_t kXTable = 16384;        // their fp16 scores in LDS
+constexpr uint32_t kXBatch = 8;            // prefetched row loads per thread
+constexpr uint32_t kNoX = 0xffffu;
+// finish_kernel's reused LDS region (32-bit words): the runs and their side
+// keys, then the candidate tables, then (fallback) the pair table; info1
+// lies past the pair table and survives it.
+constexpr uint32_t kRegSide = kMaxRuns * kRunPitch;            // runs: row keys (u16)
+constexpr uint32_t kRegWords = kRegSide + kMaxRuns * kSidePitch / 2;
+constexpr uint32_t kRegInfoSlot = 8192;                        // u4v [kSortCap]: info per slot
+constexpr uint32_t kRegXTable = kRegInfoSlot + 4 * kSortCap;   // u16 [kXTable]
+constexpr uint32_t kRegInfo1 = kRegXTable + kXTable / 2;       // u4v [kSplitMaxK]: info per stage-1 rank
+static_assert(kRegInfo1 + 4 * kSplitMaxK <= kRegWords, "finish LDS region");
+static_assert(kPairTable / 2 <= kRegInfo1 && kMaxRuns * kRun / 2 <= kRegInfoSlot, "finish LDS aliasing");
+
+struct RunsPlan {
+  Layout L;
+  uint32_t A, nc, K;
+  uint32_t runs;          // runs per image: ceil(A / kRun)
+  uint32_t q;             // prefix length whose run prefixes hold K records (host: A and K only)
+  uint32_t rows_per;      // finish: stage-1 ranks per gather pass, kFinishThreads / nc
+  int32_t agnostic;
+  int32_t vec_classes;    // anchors contiguous in aligned 16-byte groups
+  uint32_t* runs_rec;     // [B, runs, kRun]: sorted records
+  uint16_t* runs_side;    // [B, runs, kRun]: row key of each record's anchor
+  u4v* info;              // [B, A] halves: box[4], class-max bits, class, second key, second class
+  uint32_t* out;          // [B, K, 6] fp32 bits
+  thin_select_trace tr;
+};
+
+// The middle of three (a v_med3_u32).
+__device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
+  return max(min(a, b), min(max(a, b), c));
+}
+__device__ __forceinline__ uint32_t half_of(const u4v& v, uint32_t i) { return (v[i / 2] >> (16 * (i & 1))) & 0xffffu; }
+// Key 0 (NaN) and 0x7fff (zero) stand for several encodings; every other
+// key is one fp16 encoding, score_key's inverse.
+__device__ __forceinline__ bool key_ambiguous(uint32_t k) { return k == 0u || k == 0x7fffu; }
+__device__ __forceinline__ uint32_t key_bits(uint32_t k) { return k > 0x7fffu ? k : 0x7fffu - k; }
+
+// One bitonic exchange with the lane J away (J < 64): the lower lane of the
+// pair keeps the minimum when `up`, the maximum otherwise.  Whole waves only.
+template <uint32_t J>
+__device__ __forceinline__ uint32_t bitonic_xchg(uint32_t x, bool up) {
+  const uint32_t p = dev::lane_xor_bits<J>(x);
+  const bool keep_min = ((threadIdx.x & J) == 0) == up;
+  return keep_min ? min(x, p) : max(x, p);
+}
+// The in-wave end of a bitonic merge: exchanges at J, J / 2, ..., 1.
+template <uint32_t J>
+__device__ __forceinline__ uint32_t bitonic_tail(uint32_t x, bool up) {
+  if constexpr (J == 0) {
+    return x;
+  } else {
+    return bitonic_tail<J / 2>(bitonic_xchg<J>(x, up), up);
+  }
+}
+// Sorts the wave's 64 records, ascending where bit 6 of n (the record's index
+// in the block's sequence) is clear and descending where it is set: the
+// first six merges of a bitonic sort of the whole sequence.
+template <uint32_t K = 2>
+__device__ __forceinline__ uint32_t bitonic_wave(uint32_t x, uint32_t n) {
+  if constexpr (K > 64) {
+    return x;
+  } else {
+    return bitonic_wave<K * 2>(bitonic_tail<K / 2>(x, (n & K) == 0), n);
+  }
+}
+
+// Sorts buf[0, n) ascending, n a power of two in [64, 256], thread i holding
+// record i; exchanges of 64 and more go through xch (2 x kSortCap words,
+// alternate halves, so one barrier per stage).  Every thread of the block
+// calls it after a barrier that published buf; ends with a barrier.
+__device__ __forceinline__ void block_sort1(uint32_t* buf, uint32_t n, uint32_t* xch) {
+  const uint32_t tid = threadIdx.x;
+  const bool live = tid < n;  // whole waves
+  uint32_t x = kPad;
+  if (live) x = bitonic_wave(buf[tid], tid);
+  uint32_t half = 0;
+  for (uint32_t k = 128; k <= n; k <<= 1) {
+    const bool up = (tid & k) == 0;
+    for (uint32_t j = k >> 1; j >= 64; j >>= 1) {
+      uint32_t* s = xch + half;
+      half ^= kSortCap;
+      if (live) s[tid] = x;
+      __syncthreads();
+      if (live) {
+        const uint32_t p = s[tid ^ j];
+        const bool keep_min = ((tid & j) == 0) == up;
+        x = keep_min ? min(x, p) : max(x, p);
+      }
+    }
+    if (live) x = bitonic_tail<32>(x, up);
+  }
+  if (live) buf[tid] = x;
+  __syncthreads();
+}
+
+// One stage (merge size K, distance J) of a bitonic sort of 256 * E records,
+// thread t < 256 holding records t * E .. t * E + E - 1 in x.
+template <uint32_t E, uint32_t K, uint32_t J>
+__device__ __forceinline__ void bitonic_stage(uint32_t (&x)[E], bool live, uint32_t* xch, uint32_t& half) {
+  const uint32_t tid = threadIdx.x;
+  if constexpr (J < E) {  // within the thread
+    if (live) {
+#pragma unroll
+      for (uint32_t e = 0; e < E; ++e)
+        if ((e & J) == 0) {
+          const bool up = ((tid * E + e) & K) == 0;  // constant when K <= E
+          const uint32_t lo = min(x[e], x[e | J]), hi = max(x[e], x[e | J]);
+          x[e] = up ? lo : hi;
+          x[e | J] = up ? hi : lo;
+        }
+    }
+  } else if constexpr (J < 64 * E) {  // within the wave: lane xor J / E
+    if (live) {
+      const bool up = ((tid * E) & K) == 0;
+      const bool keep_min = ((tid & (J / E)) == 0) == up;
+#pragma unroll
+      for (uint32_t e = 0; e < E; ++e) {
+        const uint32_t p = dev::lane_xor_bits<J / E>(x[e]);
+        x[e] = keep_min ? min(x[e], p) : max(x[e], p);
+      }
+    }
+  } else {  // between waves, through LDS
+    uint32_t* s = xch + half;
+    half ^= kSortCap;
+    if (live) {
+#pragma unroll
+      for (uint32_t e = 0; e < E; ++e) s[tid * E + e] = x[e];
+    }
+    __syncthreads();
+    if (live) {
+      const bool up = ((tid * E) & K) == 0;
+#pragma unroll
+      for (uint32_t e = 0; e < E; ++e) {
+        const uint32_t n = tid * E + e;
+        const uint32_t p = s[n ^ J];
+        const bool keep_min = ((n & J) == 0) == up;
+        x[e] = keep_min ? min(x[e], p) : max(x[e], p);
+      }
+    }
+  }
+}
+template <uint32_t E, uint32_t K, uint32_t J>
+__device__ __forceinline__ void bitonic_merge(uint32_t (&x)[E], bool live, uint32_t* xch, uint32_t& half) {
+  if constexpr (J >= 1) {
+    bitonic_stage<E, K, J>(x, live, xch, half);
+    bitonic_merge<E, K, J / 2>(x, live, xch, half);
+  }
+}
+template <uint32_t E, uint32_t K = 2>
+__device__ __forceinline__ void bitonic_sort(uint32_t (&x)[E], bool live, uint32_t* xch, uint32_t& half) {
+  if constexpr (K <= 256 * E) {
+    bitonic_merge<E, K, K / 2>(x, live, xch, half);
+    bitonic_sort<E, K * 2>(x, live, xch, half);
+  }
+}
+// Sorts buf[0, 256 * E) ascending; same contract as block_sort1.
+template <uint32_t E>
+__device__ __forceinline__ void block_sort_e(uint32_t* buf, uint32_t* xch) {
+  const uint32_t tid = threadIdx.x;
+  const bool live = tid < 256;  // waves 0-3
+  uint32_t x[E];
+  if (live) {
+#pragma unroll
+    for (uint32_t e = 0; e < E; ++e) x[e] = buf[tid * E + e];
+  }
+  uint32_t half = 0;
+  bitonic_sort<E>(x, live, xch, half);
+  if (live) {
+#pragma unroll
+    for (uint32_t e = 0; e < E; ++e) buf[tid * E + e] = x[e];
+  }
+  __syncthreads();
+}
+// Sorts buf[0, n) ascending, n a power of two in [64, kSortCap].
+__device__ __forceinline__ void block_sort(uint32_t* buf, uint32_t n, uint32_t* xch) {
+  if (n <= 256) block_sort1(buf, n, xch);
+  else if (n == 512) block_sort_e<2>(buf, xch);
+  else block_sort_e<4>(buf, xch);
+}
+
+__device__ __forceinline__ uint32_t pow2_at_least(uint32_t n) {
+  uint32_t p = 64;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+// The K-th smallest (K >= 1) of the unique records a traversal visits, by
+// four 8-bit digits, most significant first: each pass counts the digits of
+// the records that match the digits chosen so far (a wave whose matching
+// lanes share one digit adds once), and wave 0 finds the digit where the
+// running count reaches K.  visit(f) calls f(rec) on the calling thread's
+// share of the records.  Every thread of the block calls it; hist: 256 words
+// of LDS, sel: 2.
+template <typename Visit>
+__device__ uint32_t radix_select(Visit visit, uint32_t K, uint32_t* hist, uint32_t* sel) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  uint32_t prefix = 0, kk = K;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    const uint32_t hi = shift == 24 ? 0u : ~0u << (shift + 8);
+    if (tid < 256) hist[tid] = 0;
+    __syncthreads();
+    visit([&](uint32_t rec) {
+      const bool match = (rec & hi) == (prefix & hi);
+      const uint32_t d = (rec >> shift) & 255u;
+      const uint64_t act = __ballot(match);
+      if (!act) return;
+      const uint32_t first = (uint32_t)__builtin_ctzll(act);
+      const uint32_t d0 = (uint32_t)__builtin_amdgcn_readlane((int)d, (int)first);
+      const uint64_t same = __ballot(match && d == d0);
+      if (same == act) {
+        if (lane == first) atomicAdd(&hist[d0], (uint32_t)__popcll(act));
+      } else if (match) {
+        atomicAdd(&hist[d], 1u);
+      }
+    });
+    __syncthreads();
+    if (tid < 64) {
+      uint32_t h[4], s = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h[i] = hist[tid * 4 + i];
+        s += h[i];
+      }
+      const uint32_t incl = wave_scan_u32(s);
+      uint32_t cum = incl - s;
+      if (cum < kk && kk <= incl) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (kk <= cum + h[i]) {
+            sel[0] = tid * 4 + i;
+            sel[1] = kk - cum;
+            break;
+          }
+          cum += h[i];
+        }
+      }
+    }
+    __syncthreads();
+    prefix |= sel[0] << shift;
+    kk = sel[1];
+  }
+  return prefix;
+}
+
+// Folds (key << 16 | class) k of a later class, score bits h, into the three
+// smallest so far (b < s < t; kPad where missing): every key is distinct, so
+// the new third is the middle of (s, k, t) and the new second the middle of
+// (b, k, s).
+__device__ __forceinline__ void fold3(uint32_t& b, uint32_t& s, uint32_t& t, uint32_t& bits, uint32_t k, uint32_t h) {
+  t = umed3(s, k, t);
+  s = umed3(b, k, s);
+  if (k < b) {
+    b = k;
+    bits = h;
+  }
+}
+
+// Class keys of kRun anchors (the two load forms of slice_kernel) and their
+// box channels; then the run's records sorted: waves 0 and 1 sort 64 each
+// (ascending, descending), one LDS exchange at distance 64 and the in-wave
+// end of the last merge.
+__global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
+  constexpr uint32_t kTiles = kRun / 64;                  // scalar form: 64-anchor tiles
+  constexpr uint32_t kGroups = kRunThreads / kRun;        // scalar form: class groups per anchor
+  constexpr uint32_t kUnroll = 16;                        // scalar form: class loads in flight per lane
+  constexpr uint32_t kOctets = kRun / 8;
+  constexpr uint32_t kVGroups = kRunThreads / kOctets;    // vector form: class groups per octet
+  constexpr uint32_t kVUnroll = 4;                        // vector form: 16-byte loads in flight per lane
+  constexpr uint32_t kParts = kRunThreads / kRun;         // group-reduction parts per anchor
+  static_assert(kVGroups == kParts * 8 && kGroups == kParts && kGroups == 4, "group reduction shape");
+  // per class group and anchor: the three smallest (key << 16 | class), best bits
+  __shared__ uint32_t g_b[kVGroups * kRun], g_s[kVGroups * kRun], g_t[kVGroups * kRun];
+  __shared__ uint16_t g_bits[kVGroups * kRun];
+  __shared__ uint32_t part_b[kParts * kRun], part_s[kParts * kRun], part_t[kParts * kRun];
+  __shared__ uint16_t part_bits[kParts * kRun];
+  __shared__ uint16_t box[4 * kRun];
+  __shared__ uint16_t side_of[kRun];
+  __shared__ uint32_t xch[kRun];
+  const uint32_t b = blockIdx.y, run = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* img = p.L.x + b * p.L.sb;
+  const uint32_t sc = (uint32_t)p.L.sc;
+  if (p.vec_classes) {
+    const uint32_t o = tid % kOctets, g = tid / kOctets;
+    const uint32_t a0 = run * kRun + o * 8u;
+    uint32_t kb[8], ks[8], kt[8], bits[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kb[j] = kPad;
+      ks[j] = kPad;
+      kt[j] = kPad;
+      bits[j] = 0;
+    }
+    if (a0 < p.A) {  // A % 8 == 0: the octet is whole
+      // box channel g of the octet (groups 0-3), in flight with the classes
+      const u4v bv = *reinterpret_cast<const u4v*>(img + min(g, 3u) * sc + a0);
+      for (uint32_t c0 = g; c0 < p.nc; c0 += kVGroups * kVUnroll) {
+        u4v v[kVUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kVUnroll; ++u) {
+          const uint32_t c = c0 + u * kVGroups;
+          v[u] = c < p.nc ? *reinterpret_cast<const u4v*>(img + (4u + c) * sc + a0) : (u4v)0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kVUnroll; ++u) {
+          const uint32_t c = c0 + u * kVGroups;
+          if (c < p.nc) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t h = half_of(v[u], j);
+              fold3(kb[j], ks[j], kt[j], bits[j], (score_key(h) << 16) | c, h);
+            }
+          }
+        }
+      }
+      if (g < 4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) box[g * kRun + o * 8 + j] = (uint16_t)half_of(bv, j);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t at = g * kRun + o * 8 + j;
+      g_b[at] = kb[j];
+      g_s[at] = ks[j];
+      g_t[at] = kt[j];
+      g_bits[at] = (uint16_t)bits[j];
+    }
+  } else {
+    const uint32_t lane = tid & 63u, wave = tid >> 6;
+    const uint32_t local = (wave % kTiles) * 64u + lane, grp = wave / kTiles;
+    const uint32_t a = run * kRun + local;
+    uint32_t kb = kPad, ks = kPad, kt = kPad, bb = 0u;
+    if (a < p.A) {
+      // one image spans fewer than 2^31 elements (checked on the host)
+      const uint32_t base = a * (uint32_t)p.L.sa;
+      const uint32_t bxv = img[base + grp * sc];  // box channel grp
+      const uint32_t row = base + 4u * sc;
+      for (uint32_t c0 = grp; c0 < p.nc; c0 += kGroups * kUnroll) {
+        uint32_t bits[kUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kUnroll; ++u) {
+          const uint32_t c = c0 + u * kGroups;
+          bits[u] = c < p.nc ? img[row + c * sc] : 0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kUnroll; ++u) {
+          const uint32_t c = c0 + u * kGroups;
+          if (c < p.nc) fold3(kb, ks, kt, bb, (score_key(bits[u]) << 16) | c, bits[u]);
+        }
+      }
+      box[grp * kRun + local] = (uint16_t)bxv;
+    }
+    const uint32_t at = grp * kRun + local;
+    g_b[at] = kb;
+    g_s[at] = ks;
+    g_t[at] = kt;
+    g_bits[at] = (uint16_t)bb;
+  }
+  __syncthreads();
+  // The three smallest over the class groups of each anchor (all keys
+  // distinct, so any merge order gives the same three); the vector form's 32
+  // groups reduce in two levels.
+  auto reduce = [&](const uint32_t* bs, const uint32_t* ss, const uint32_t* ts, const uint16_t* hs, auto count,
+                    uint32_t first, uint32_t& kb, uint32_t& ks, uint32_t& kt, uint32_t& bb) {
+    constexpr uint32_t N = decltype(count)::value;
+    uint32_t vb[N], vs[N], vt[N], vh[N];
+#pragma unroll
+    for (uint32_t g = 0; g < N; ++g) {
+      const uint32_t at = (first + g) * kRun;
+      vb[g] = bs[at];
+      vs[g] = ss[at];
+      vt[g] = ts[at];
+      vh[g] = hs[at];
+    }
+    kb = vb[0];
+    ks = vs[0];
+    kt = vt[0];
+    bb = vh[0];
+#pragma unroll
+    for (uint32_t g = 1; g < N; ++g) {
+      fold3(kb, ks, kt, bb, vb[g], vh[g]);
+      uint32_t unused = 0;
+      fold3(kb, ks, kt, unused, vs[g], 0u);  // never below the group's best, so bits stay
+      fold3(kb, ks, kt, unused, vt[g], 0u);
+    }
+  };
+  uint32_t kb = kPad, ks = kPad, kt = kPad, bb = 0u;
+  if (p.vec_classes) {
+    const uint32_t x = tid % kRun, q = tid / kRun;
+    reduce(g_b + x, g_s + x, g_t + x, g_bits + x, std::integral_constant<uint32_t, 8>(), q * 8u, kb, ks, kt, bb);
+    part_b[q * kRun + x] = kb;
+    part_s[q * kRun + x] = ks;
+    part_t[q * kRun + x] = kt;
+    part_bits[q * kRun + x] = (uint16_t)bb;
+    __syncthreads();
+    if (tid < kRun)
+      reduce(part_b + tid, part_s + tid, part_t + tid, part_bits + tid, std::integral_constant<uint32_t, kParts>(), 0u,
+             kb, ks, kt, bb);
+  } else if (tid < kRun) {
+    reduce(g_b + tid, g_s + tid, g_t + tid, g_bits + tid, std::integral_constant<uint32_t, kGroups>(), 0u, kb, ks, kt,
+           bb);
+  }
+  uint32_t rec = kPad;
+  if (tid < kRun) {
+    const uint32_t a = run * kRun + tid;
+    if (a < p.A) {
+      const size_t t = (size_t)b * p.A + a;
+      u4v iv;
+      iv[0] = box[tid] | ((uint32_t)box[kRun + tid] << 16);
+      iv[1] = box[2 * kRun + tid] | ((uint32_t)box[3 * kRun + tid] << 16);
+      iv[2] = bb | (kb << 16);                    // class-max bits, class
+      iv[3] = (ks >> 16) | (ks << 16);            // second key, second class (0xffff, 0xffff: none)
+      p.info[t] = iv;
+      if (p.tr.class_max) static_cast<uint16_t*>(p.tr.class_max)[t] = (uint16_t)bb;
+      rec = (kb & 0xffff0000u) | a;
+    }
+    const uint32_t sk = ks >> 16;
+    side_of[tid] = (uint16_t)min(kt >> 16, key_ambiguous(sk) ? sk : 0xffffu);
+    rec = bitonic_wave(rec, tid);
+    xch[tid] = rec;
+  }
+  __syncthreads();
+  if (tid < kRun) {
+    const uint32_t o = xch[tid ^ 64u];
+    rec = (tid & 64u) ? max(rec, o) : min(rec, o);
+    rec = bitonic_tail<32>(rec, true);
+    const size_t at = ((size_t)b * p.runs + run) * kRun + tid;
+    p.runs_rec[at] = rec;
+    p.runs_side[at] = rec == kPad ? (uint16_t)0xffffu : side_of[(rec & 0xffffu) - run * kRun];
+  }
+}
+
+// Stage-1 candidates, their sort, stage 2 and the rows, for image blockIdx.x.
+__global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
+  __shared__ __attribute__((aligned(16))) uint32_t region[kRegWords];
+  __shared__ uint32_t sortbuf[kSortCap], s2buf[kSortCap + 64];
+  __shared__ uint32_t xch[2 * kSortCap];
+  __shared__ uint16_t anchor_of[kSortCap], xslot[kSortCap], xlist[kMaxX], xrank[kSortCap], anchors1[kSplitMaxK],
+      x1[kSplitMaxK];
+  __shared__ uint32_t cnt[kMaxRuns], off[kMaxRuns + 1];
+  __shared__ uint32_t hist[256], sel[2], bound, count, count2, nx, nxr;
+  const uint32_t b = blockIdx.x, tid = threadIdx.x, nl = p.runs, K = p.K, nc = p.nc;
+  const uint16_t* img = p.L.x + b * p.L.sb;
+  const uint32_t sa = (uint32_t)p.L.sa, sc = (uint32_t)p.L.sc;
+  uint32_t* lists = region;
+  uint16_t* lside = reinterpret_cast<uint16_t*>(region + kRegSide);
+  u4v* info_slot = reinterpret_cast<u4v*>(region + kRegInfoSlot);
+  uint16_t* xtable = reinterpret_cast<uint16_t*>(region + kRegXTable);
+  u4v* info1 = reinterpret_cast<u4v*>(region + kRegInfo1);
+  uint16_t* table = reinterpret_cast<uint16_t*>(region);  // fallback: [K * nc]
+  const u4v* info_g = p.info + (size_t)b * p.A;
+
+  // the runs and their row keys into LDS: every 16-byte load issued before
+  // any is stored
+  {
+    constexpr uint32_t kV = kRun / 4, kPer = kMaxRuns * kV / kFinishThreads;
+    constexpr uint32_t kSV = kRun / 8, kSPer = kMaxRuns * kSV / kFinishThreads;
+    const uint32_t total = nl * kV, stotal = nl * kSV;
+    const u4v* src = reinterpret_cast<const u4v*>(p.runs_rec + (size_t)b * nl * kRun);
+    const u4v* ssrc = reinterpret_cast<const u4v*>(p.runs_side + (size_t)b * nl * kRun);
+    u4v v[kPer], sv[kSPer];
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i)
+      if (tid + i * kFinishThreads < total) v[i] = src[tid + i * kFinishThreads];
+#pragma unroll
+    for (uint32_t i = 0; i < kSPer; ++i)
+      if (tid + i * kFinishThreads < stotal) sv[i] = ssrc[tid + i * kFinishThreads];
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+      const uint32_t e = tid + i * kFinishThreads;
+      if (e < total) reinterpret_cast<u4v*>(lists)[(e / kV) * (kRunPitch / 4) + e % kV] = v[i];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kSPer; ++i) {
+      const uint32_t e = tid + i * kFinishThreads;
+      if (e < stotal) reinterpret_cast<u4v*>(lside)[(e / kSV) * (kSidePitch / 8) + e % kSV] = sv[i];
+    }
+  }
+  if (tid == 0) {
+    count = 0;
+    count2 = 0;
+    nx = 0;
+    nxr = 0;
+  }
+  __syncthreads();
+
+  // Candidates: records up to R, the largest of the prefix ends (the first
+  // min(q, len) records of each run hold at least K records, so the K-th
+  // smallest is at most R).  Wave 0, lane t: runs t and t + 64; the count
+  // past the prefix scans 16 records a step.
+  if (tid < 64) {
+    uint32_t len[2], m[2], R = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t l = tid + 64u * h;
+      len[h] = l < nl ? min(kRun, p.A - l * kRun) : 0u;
+      m[h] = min(p.q, len[h]);
+      if (m[h]) R = max(R, lists[l * kRunPitch + m[h] - 1]);
+    }
+    R = wave_max_u32(R);
+    uint32_t c[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t* lp = lists + (tid + 64u * h) * kRunPitch;
+      const uint32_t n = len[h];
+      c[h] = m[h];  // the first m records are at most R
+      while (c[h] < n) {
+        const uint32_t c4 = c[h] & ~3u;
+        uint32_t hit = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < 4; ++u) {
+          const uint32_t at = c4 + 4 * u;
+          const u4v v = at < n ? reinterpret_cast<const u4v*>(lp)[at / 4] : (u4v)kPad;
+          hit += (v.x <= R) + (v.y <= R) + (v.z <= R) + (v.w <= R);
+        }
+        const uint32_t before = c[h] - c4;  // records of the first vector already counted
+        const uint32_t found = hit - min(hit, before);
+        c[h] = min(c[h] + found, n);
+        if (found < 16 - before) break;
+      }
+    }
+    const uint32_t incl0 = wave_scan_u32(c[0]);
+    const uint32_t total0 = (uint32_t)__builtin_amdgcn_readlane((int)incl0, 63);
+    const uint32_t incl1 = wave_scan_u32(c[1]) + total0;
+    if (tid < nl) {
+      cnt[tid] = c[0];
+      off[tid] = incl0 - c[0];
+    }
+    if (tid + 64 < nl) {
+      cnt[tid + 64] = c[1];
+      off[tid + 64] = incl1 - c[1];
+    }
+    if (tid == 63) {
+      off[kMaxRuns] = incl1;
+      bound = R;
+    }
+  }
+  __syncthreads();
+  const uint32_t C = off[kMaxRuns], Rkey = bound >> 16;
+  // eight threads per run walk its candidates
+  auto candidates = [&](auto&& f) {
+    const uint32_t l = tid >> 3;
+    if (l < nl) {
+      const uint32_t n = cnt[l], at = off[l];
+      for (uint32_t k = tid & 7u; k < n; k += 8) f(lists[l * kRunPitch + k], lside[l * kSidePitch + k], at + k);
+    }
+  };
+  const bool few = C <= kSortCap;
+  uint32_t n1 = pow2_at_least(K);
+  if (few) {
+    // Candidate slots in (run, position) order, sorted as (key << 16 | slot):
+    // runs cover increasing anchor ranges and sort equal keys by anchor, so
+    // slot order among equal keys is anchor order and the sort gives the
+    // stage-1 order.  Rows to prefetch: a row key at most the bound.
+    candidates([&](uint32_t rec, uint32_t rk, uint32_t at) {
+      sortbuf[at] = (rec & 0xffff0000u) | at;
+      anchor_of[at] = (uint16_t)(rec & 0xffffu);
+      uint32_t x = kNoX;
+      if (!p.agnostic && rk <= Rkey) {
+        x = atomicAdd(&nx, 1u);
+        if (x < kMaxX) xlist[x] = (uint16_t)at;
+        else x = kNoX;
+      }
+      xslot[at] = (uint16_t)x;
+    });
+    n1 = pow2_at_least(C);
+  } else {
+    const uint32_t T = radix_select(
+        [&](auto&& f) { candidates([&](uint32_t rec, uint32_t, uint32_t) { f(rec); }); }, K, hist, sel);
+    candidates([&](uint32_t rec, uint32_t, uint32_t) {
+      if (rec <= T) {
+        const uint32_t slot = atomicAdd(&count, 1u);
+        if (slot < kSortCap) sortbuf[slot] = rec;  // exactly K (records are unique)
+      }
+    });
+  }
+  __syncthreads();
+  const uint32_t G = p.rows_per, cls = p.agnostic ? 0u : tid % nc, grow = p.agnostic ? 0u : tid / nc;
+  const uint32_t NX = nx;
+  const bool fast = few && !p.agnostic && NX <= kMaxX && NX <= kXBatch * G && NX * nc <= kXTable && !p.tr.gathered;
+  u4v my_info = (u4v)0u;
+  uint32_t xr[kXBatch];
+  if (few) {
+    // In flight across the sort (nothing reads them before it ends): the
+    // info of candidate slot tid and the prefetched rows (thread (grow, cls):
+    // class cls of rows grow, grow + G, ...).
+    if (tid < C) my_info = info_g[min((uint32_t)anchor_of[tid], p.A - 1)];
+    if (fast && grow < G) {
+#pragma unroll
+      for (uint32_t i = 0; i < kXBatch; ++i) {
+        const uint32_t x = grow + i * G;
+        if (x < NX) xr[i] = img[min((uint32_t)anchor_of[xlist[x]], p.A - 1) * sa + (4u + cls) * sc];
+      }
+    }
+  }
+  const uint32_t have1 = few ? C : K;
+  for (uint32_t i = have1 + tid; i < n1; i += kFinishThreads) sortbuf[i] = kPad;
+  __syncthreads();
+  block_sort(sortbuf, n1, xch);
+
+  if (few) {
+    // the runs are dead: the slot tables take their place
+    if (tid < C) info_slot[tid] = my_info;
+    if (fast && grow < G) {
+#pragma unroll
+      for (uint32_t i = 0; i < kXBatch; ++i) {
+        const uint32_t x = grow + i * G;
+        if (x < NX) xtable[x * nc + cls] = (uint16_t)xr[i];
+      }
+    }
+    __syncthreads();
+  }
+  // stage 1: ranks 0..K-1 (at least K real records were sorted; the clamps
+  // only keep addresses in bounds)
+  const uint32_t T1 = sortbuf[K - 1] >> 16;
+  for (uint32_t r = tid; r < K; r += kFinishThreads) {
+    const uint32_t rec = sortbuf[r];
+    u4v iv;
+    uint32_t a, x = kNoX;
+    if (few) {
+      const uint32_t s = min(rec & 0xffffu, C - 1);
+      a = anchor_of[s];
+      iv = info_slot[s];
+      x = xslot[s];
+    } else {
+      a = min(rec & 0xffffu, p.A - 1);
+      iv = info_g[a];  // many tied candidates: one more round of loads
+    }
+    anchors1[r] = (uint16_t)a;
+    if (p.tr.stage1) static_cast<int64_t*>(p.tr.stage1)[(size_t)b * K + r] = a;
+    info1[r] = iv;
+    x1[r] = (uint16_t)x;
+    if (fast) {
+      s2buf[r] = (rec & 0xffff0000u) | (r * nc + half_of(iv, 5));  // the class-max pair
+      const uint32_t sk = half_of(iv, 6);
+      if (sk <= T1) {
+        if (x != kNoX) {
+          xrank[atomicAdd(&nxr, 1u)] = (uint16_t)r;  // its row holds the extra pairs
+        } else {
+          const uint32_t slot = atomicAdd(&count2, 1u);  // the second pair only (third key above T1)
+          if (K + slot < kSortCap + 64) s2buf[K + slot] = (sk << 16) | (r * nc + half_of(iv, 7));
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  if (p.agnostic) {
+    for (uint32_t i = tid; i < K; i += kFinishThreads) {
+      const u4v iv = info1[i];
+      const uint32_t bx[4] = {half_of(iv, 0), half_of(iv, 1), half_of(iv, 2), half_of(iv, 3)};
+      put_row(p.out, p.tr, (size_t)b * K + i, bx, anchors1[i], half_of(iv, 5), half_of(iv, 4), -1);
+    }
+    return;
+  }
+
+  if (fast) {
+    // the other pairs of the prefetched rows keyed at most T1
+    const uint32_t NE = nxr;
+    if (grow < G) {
+      for (uint32_t e = grow; e < NE; e += G) {
+        const uint32_t r = xrank[e];
+        const uint32_t x = min((uint32_t)x1[r], kMaxX - 1);
+        if (cls != half_of(info1[r], 5)) {
+          const uint32_t key = score_key(xtable[x * nc + cls]);
+          if (key <= T1) {
+            const uint32_t slot = atomicAdd(&count2, 1u);
+            if (K + slot < kSortCap + 64) s2buf[K + slot] = (key << 16) | (r * nc + cls);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const uint32_t E2 = count2, S = K + E2;
+    // row i of the output: pair record rec
+    auto emit = [&](uint32_t i, uint32_t rec) {
+      const uint32_t f = min(rec & 0xffffu, K * nc - 1);  // a pair index (clamp: LDS bounds only)
+      const uint32_t r = f / nc, c = f - r * nc;
+      const u4v iv = info1[r];
+      const uint32_t x = x1[r];
+      const uint32_t sbits = c == half_of(iv, 5) ? half_of(iv, 4)
+                             : x != kNoX        ? xtable[min(x, kMaxX - 1) * nc + c]
+                                                : key_bits(half_of(iv, 6));  // the second pair
+      const uint32_t bx[4] = {half_of(iv, 0), half_of(iv, 1), half_of(iv, 2), half_of(iv, 3)};
+      put_row(p.out, p.tr, (size_t)b * K + i, bx, anchors1[r], c, sbits, f);
+    };
+    if (E2 <= 64) {
+      // The class-max pairs s2buf[0, K) are in order already (keys follow the
+      // stage-1 ranks, and so do the pair indices of equal keys); wave 0
+      // sorts the extras, and every record's row is its index plus the
+      // records of the other list below it.
+      if (tid < 64) {
+        uint32_t e = tid < E2 ? s2buf[K + tid] : kPad;
+        e = bitonic_wave(e, tid);
+        s2buf[K + tid] = e;  // s2buf holds kSortCap + 64 records
+      }
+      __syncthreads();
+      const uint32_t* ext = s2buf + K;
+      for (uint32_t i = tid; i < K + E2; i += kFinishThreads) {
+        const uint32_t rec = s2buf[i];
+        const bool cm = i < K;
+        const uint32_t* other = cm ? ext : s2buf;
+        uint32_t lo = 0, hi = cm ? E2 : K;  // records of the other list below rec
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (other[mid] < rec) lo = mid + 1;
+          else hi = mid;
+        }
+        const uint32_t row = (cm ? i : i - K) + lo;
+        if (row < K) emit(row, rec);
+      }
+      return;
+    }
+    if (S <= kSortCap) {
+      const uint32_t n2 = pow2_at_least(S);
+      for (uint32_t i = S + tid; i < n2; i += kFinishThreads) s2buf[i] = kPad;
+      __syncthreads();
+      block_sort(s2buf, n2, xch);
+      for (uint32_t i = tid; i < K; i += kFinishThreads) emit(i, s2buf[i]);
+      return;
+    }
+  }
+
+  // Fallback: every stage-1 row into the LDS table (thread (grow, cls): class
+  // cls of ranks grow, grow + G, ...); pairs keyed at most T1 survive.
+  if (tid == 0) count = 0;
+  __syncthreads();
+  if (grow < G) {
+    for (uint32_t r0 = grow; r0 < K; r0 += G * kGatherBatch) {
+      uint32_t h[kGatherBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kGatherBatch; ++u) {
+        const uint32_t r = min(r0 + u * G, K - 1);
+        h[u] = img[(uint32_t)anchors1[r] * sa + (4u + cls) * sc];
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kGatherBatch; ++u) {
+        const uint32_t r = r0 + u * G;
+        if (r < K) {
+          const uint32_t f = r * nc + cls;
+          table[f] = (uint16_t)h[u];
+          if (p.tr.gathered) static_cast<uint16_t*>(p.tr.gathered)[(size_t)b * K * nc + f] = (uint16_t)h[u];
+          const uint32_t key = score_key(h[u]);
+          if (key <= T1) {
+            const uint32_t slot = atomicAdd(&count, 1u);
+            if (slot < kSortCap) s2buf[slot] = (key << 16) | f;
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // the survivors sorted, or (more than kSortCap: ties) the K-th smallest pair
+  // record selected over the whole table and the K records up to it sorted
+  const uint32_t S = count;
+  uint32_t have2 = K;
+  if (S <= kSortCap) {
+    have2 = S;
+  } else {
+    const uint32_t total = K * nc;
+    if (tid == 0) count2 = 0;
+    const uint32_t T = radix_select(
+        [&](auto&& f) {
+          for (uint32_t i = tid; i < total; i += kFinishThreads) f((score_key(table[i]) << 16) | i);
+        },
+        K, hist, sel);
+    for (uint32_t i = tid; i < total; i += kFinishThreads) {
+      const uint32_t rec = (score_key(table[i]) << 16) | i;
+      if (rec <= T) {
+        const uint32_t slot = atomicAdd(&count2, 1u);
+        if (slot < kSortCap) s2buf[slot] = rec;  // exactly K
+      }
+    }
+  }
+  const uint32_t n2 = pow2_at_least(have2);
+  for (uint32_t i = have2 + tid; i < n2; i += kFinishThreads) s2buf[i] = kPad;
+  __syncthreads();
+  block_sort(s2buf, n2, xch);
+  for (uint32_t i = tid; i < K; i += kFinishThreads) {
+    const uint32_t f = min(s2buf[i] & 0xffffu, K * nc - 1);
+    const uint32_t r = f / nc, c = f - r * nc;
+    const u4v iv = info1[r];
+    const uint32_t bx[4] = {half_of(iv, 0), half_of(iv, 1), half_of(iv, 2), half_of(iv, 3)};
+    put_row(p.out, p.tr, (size_t)b * K + i, bx, anchors1[r], c, table[f], f);
+  }
+}
+
 // ---------------------------------------------------------------- host
 
 // Shape of the split selection for these sizes; ok == false leaves them to
@@ -1238,10 +2113,38 @@ SplitShape split_shape(int64_t B, int64_t A, int64_t nc, int64_t K, bool agnosti
   return sh;
 }
 
+// Shape of the two-launch selection; ok == false leaves the sizes to the
+// split kernels or the one-workgroup-per-batch path (K above kSplitMaxK, more
+// than kMaxRuns runs, more classes than finish_kernel threads, or K * nc pair
+// scores beyond its LDS table).
+struct RunsShape {
+  bool ok;
+  uint32_t runs, q, rows_per;
+};
+
+RunsShape runs_shape(int64_t B, int64_t A, int64_t nc, int64_t K, bool agnostic, int64_t image_extent) {
+  RunsShape r;
+  memset(&r, 0, sizeof r);
+  if (K < 1 || K > (int64_t)kSplitMaxK || A > (int64_t)(kMaxRuns * kRun) || B > 65535 ||
+      image_extent >= ((int64_t)1 << 31))
+    return r;
+  if (!agnostic && (nc > (int64_t)kFinishThreads || K * nc > (int64_t)kPairTable)) return r;
+  r.runs = (uint32_t)((A + kRun - 1) / kRun);
+  // q: the smallest prefix length whose run prefixes hold K records (every
+  // run holds kRun anchors but the last, which holds `last`)
+  const int64_t last = A - (int64_t)(r.runs - 1) * kRun;
+  const int64_t q = (K + r.runs - 1) / r.runs;
+  r.q = (uint32_t)(q <= last ? q : (K - last + r.runs - 2) / (r.runs - 1));
+  r.rows_per = agnostic ? 0u : (uint32_t)(kFinishThreads / nc);
+  r.ok = true;
+  return r;
+}
+
 struct WsLayout {
-  size_t bits1, cls1, stage1, gathered, stage2, thresh, recs, lists1, lists2, count2, total;
+  size_t bits1, cls1, stage1, gathered, stage2, thresh, recs, lists1, lists2, count2, runs, runs_side, info, total;
   uint32_t recs_pitch;  // P for the large-K path (0 = not needed)
   SplitShape split;
+  RunsShape two;        // the two-launch selection (taken before split when ok)
 };
 
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1253,7 +2156,8 @@ WsLayout ws_layout(int64_t B, int64_t A, int64_t nc, int64_t max_det, bool agnos
   WsLayout w;
   memset(&w, 0, sizeof w);
   const int64_t K = max_det < A ? max_det : A;
-  w.split = split_shape(B, A, nc, K, agnostic, image_extent < 0 ? 0 : image_extent);
+  w.two = runs_shape(B, A, nc, K, agnostic, image_extent < 0 ? 0 : image_extent);
+  if (!w.two.ok) w.split = split_shape(B, A, nc, K, agnostic, image_extent < 0 ? 0 : image_extent);
   size_t off = 0;
   w.bits1 = off; off += up256((size_t)(B * A) * 2);
   w.cls1 = off; off += up256((size_t)(B * A) * 4);
@@ -1262,6 +2166,11 @@ WsLayout ws_layout(int64_t B, int64_t A, int64_t nc, int64_t max_det, bool agnos
     w.gathered = off; off += up256((size_t)(B * K * nc) * 2);
     w.stage2 = off; off += up256((size_t)(B * K) * 4);
     w.thresh = off; off += up256((size_t)B * 4);
+  }
+  if (w.two.ok) {
+    w.runs = off; off += up256((size_t)B * w.two.runs * kRun * 4);
+    w.runs_side = off; off += up256((size_t)B * w.two.runs * kRun * 2);
+    w.info = off; off += up256((size_t)(B * A) * 16);
   }
   if (w.split.ok) {
     w.lists1 = off; off += up256((size_t)B * w.split.lists1 * kSlice * 4);
@@ -1371,6 +2280,32 @@ thin_status select_run(const thin_desc* decoded, int64_t max_det, bool agn, void
 
   Layout L{static_cast<const uint16_t*>(decoded->data), decoded->strides[0], decoded->strides[1],
            decoded->strides[2]};
+  const bool vec_classes = decoded->strides[1] == 1 && A % 8 == 0 && decoded->strides[2] % 8 == 0 &&
+                           (B == 1 || decoded->strides[0] % 8 == 0) &&
+                           reinterpret_cast<uintptr_t>(decoded->data) % 16 == 0;
+  if (w.two.ok) {
+    RunsPlan rp;
+    memset(&rp, 0, sizeof rp);
+    rp.L = L;
+    rp.A = (uint32_t)A;
+    rp.nc = (uint32_t)nc;
+    rp.K = (uint32_t)K;
+    rp.runs = w.two.runs;
+    rp.q = w.two.q;
+    rp.rows_per = w.two.rows_per;
+    rp.agnostic = agn ? 1 : 0;
+    rp.vec_classes = vec_classes ? 1 : 0;
+    rp.runs_rec = reinterpret_cast<uint32_t*>(ws + w.runs);
+    rp.runs_side = reinterpret_cast<uint16_t*>(ws + w.runs_side);
+    rp.info = reinterpret_cast<u4v*>(ws + w.info);
+    rp.out = static_cast<uint32_t*>(out);
+    rp.tr = tr;
+    hipLaunchKernelGGL(runs_kernel, dim3(rp.runs, (uint32_t)B), dim3(kRunThreads), 0, stream, rp);
+    THIN_LAUNCH_CHECK("select_runs");
+    hipLaunchKernelGGL(finish_kernel, dim3((uint32_t)B), dim3(kFinishThreads), 0, stream, rp);
+    THIN_LAUNCH_CHECK("select_finish");
+    return THIN_OK;
+  }
   if (w.split.ok) {
     SplitPlan sp;
     memset(&sp, 0, sizeof sp);
@@ -1385,9 +2320,7 @@ thin_status select_run(const thin_desc* decoded, int64_t max_det, bool agn, void
     sp.pitch2 = w.split.pitch2;
     sp.lds_pitch2 = w.split.lds_pitch2;
     sp.agnostic = agn ? 1 : 0;
-    sp.vec_classes = decoded->strides[1] == 1 && A % 8 == 0 && decoded->strides[2] % 8 == 0 &&
-                     (B == 1 || decoded->strides[0] % 8 == 0) &&
-                     reinterpret_cast<uintptr_t>(decoded->data) % 16 == 0;
+    sp.vec_classes = vec_classes ? 1 : 0;
     sp.bits1 = bits1;
     sp.cls1 = cls1;
     sp.lists1_rec = reinterpret_cast<uint32_t*>(ws + w.lists1);
