@@ -30,6 +30,12 @@ def run_case(gpu, x, max_det, agnostic, layout, name):
         assert bits_equal(got, exp.to(got.dtype)), f"{name}: {mine}"
     plain = capi.detection_select(dv, max_det, agnostic)
     assert bits_equal(plain.cpu(), ref["output"]), f"{name}: production != trace"
+    # every stage but the gathered scores (whose trace takes the full gather)
+    partial = [n for n in STAGES if n != "gathered"]
+    out2, tr2 = capi.detection_select(dv, max_det, agnostic, trace=partial)
+    assert bits_equal(out2.cpu(), ref["output"]), f"{name}: output (partial trace)"
+    for mine in partial:
+        assert bits_equal(tr2[mine].cpu(), ref[STAGES[mine]].to(tr2[mine].dtype)), f"{name}: {mine} (partial trace)"
     return ref, v
 
 
@@ -63,3 +69,52 @@ def test_selection_batched_and_workspace_errors(gpu):
     st = capi.lib().thin_detection_select(capi.ctypes.byref(capi.desc(d)), 300, 0, out.data_ptr(),
                                           ws.data_ptr(), 16, None, torch.cuda.current_stream().cuda_stream)
     assert st == 4 and b"workspace" in capi.lib().thin_last_error()
+
+
+def _pair_case(kind, seed):
+    """Inputs that steer stage 2 through each of its forms: every stage-1
+    anchor with a second class at its best score (more second pairs than one
+    wave merges), a few anchors with four classes at the top (their rows
+    prefetched, few extras), forty such anchors (many extras), and NaN and
+    signed-zero second scores (bits the key does not fix)."""
+    g = torch.Generator().manual_seed(seed)
+    if kind == "second-pairs":
+        a, nc = 2000, 10
+        s = torch.rand(1, a, nc, generator=g) * 0.1
+        v = 0.5 + 0.5 * torch.rand(1, a, generator=g)
+        c = torch.stack([torch.randperm(nc, generator=g)[:2] for _ in range(a)])
+        s[0, torch.arange(a)[:, None], c] = v[0][:, None]
+    elif kind in ("row-extras", "many-row-extras"):
+        a, nc = 3000, 20
+        s = torch.rand(1, a, nc, generator=g) * 0.9
+        n = 10 if kind == "row-extras" else 40
+        rows = torch.randperm(a, generator=g)[:n]
+        for r in rows.tolist():
+            s[0, r, torch.randperm(nc, generator=g)[:4]] = 0.995
+    else:  # "ambiguous-seconds"
+        a, nc = 64, 6
+        s = -torch.rand(1, a, nc, generator=g)
+        for r in range(0, a, 4):
+            s[0, r, 1] = float("nan")
+            s[0, r, 4] = float("nan")
+        for r in range(1, a, 4):
+            s[0, r, 0] = -0.0
+            s[0, r, 3] = 0.0
+        for r in range(2, a, 4):
+            s[0, r, 2] = 0.0
+            s[0, r, 5] = -0.0
+    sh = s.half()
+    if kind == "ambiguous-seconds":  # NaN payloads differ
+        bits = sh.view(torch.int16)
+        bits[0, 0::4, 1] = 0x7E01
+        bits[0, 0::4, 4] = -0x0200  # 0xFE00
+    boxes = torch.randn(1, a, 4, generator=g).half()
+    return torch.cat((boxes, sh), -1)
+
+
+@pytest.mark.parametrize("layout", ["transposed", "contiguous"])
+@pytest.mark.parametrize("kind,max_det", [("second-pairs", 300), ("row-extras", 300), ("many-row-extras", 300),
+                                          ("ambiguous-seconds", 64)])
+def test_selection_pair_paths(gpu, kind, max_det, layout):
+    x = _pair_case(kind, 31)
+    run_case(gpu, x, max_det, False, layout, f"{kind}-{layout}")

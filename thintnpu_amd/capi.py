@@ -332,7 +332,8 @@ def detection_select(decoded, max_det: int, agnostic: bool = False, trace: bool 
                      stream=None, out=None, workspace=None, noalloc: bool = False):
     """thin_detection_select with a workspace (given, or allocated here), or,
     with noalloc=True, thin_detection_select_noalloc on the library's static
-    scratch (no workspace argument)."""
+    scratch (no workspace argument).  trace: True for every trace stage, or
+    a collection of stage names for those only (the others stay null)."""
     b, a, ch = decoded.shape
     nc = ch - 4
     k = min(max_det, a)
@@ -354,6 +355,8 @@ def detection_select(decoded, max_det: int, agnostic: bool = False, trace: bool 
             anchors=torch.empty((b, k), dtype=torch.int64, device=dev),
             labels=torch.empty((b, k), dtype=torch.int64, device=dev),
         )
+        if trace is not True:
+            tensors = {n: t for n, t in tensors.items() if n in set(trace)}
         tr = ThinSelectTrace(**{n: (t.data_ptr() if t.numel() else None) for n, t in tensors.items()})
     trace_arg = ctypes.byref(tr) if tr is not None else None
     out_ptr = out.data_ptr() if out.numel() else None

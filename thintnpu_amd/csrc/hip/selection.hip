@@ -1721,7 +1721,7 @@ __global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
 // Stage-1 candidates, their sort, stage 2 and the rows, for image blockIdx.x.
 __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
   __shared__ __attribute__((aligned(16))) uint32_t region[kRegWords];
-  __shared__ uint32_t sortbuf[kSortCap], s2buf[kSortCap + 64];
+  __shared__ uint32_t sortbuf[kSortCap], s2buf[kSortCap + 64];  // s2buf: K pairs and up to 64 extras
   __shared__ uint32_t xch[2 * kSortCap];
   __shared__ uint16_t anchor_of[kSortCap], xslot[kSortCap], xlist[kMaxX], xrank[kSortCap], anchors1[kSplitMaxK],
       x1[kSplitMaxK];
@@ -1852,6 +1852,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
       xslot[at] = (uint16_t)x;
     });
     n1 = pow2_at_least(C);
+    for (uint32_t i = C + tid; i < n1; i += kFinishThreads) sortbuf[i] = kPad;
   } else {
     const uint32_t T = radix_select(
         [&](auto&& f) { candidates([&](uint32_t rec, uint32_t, uint32_t) { f(rec); }); }, K, hist, sel);
@@ -1861,6 +1862,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
         if (slot < kSortCap) sortbuf[slot] = rec;  // exactly K (records are unique)
       }
     });
+    for (uint32_t i = K + tid; i < n1; i += kFinishThreads) sortbuf[i] = kPad;
   }
   __syncthreads();
   const uint32_t G = p.rows_per, cls = p.agnostic ? 0u : tid % nc, grow = p.agnostic ? 0u : tid / nc;
@@ -1881,9 +1883,6 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
       }
     }
   }
-  const uint32_t have1 = few ? C : K;
-  for (uint32_t i = have1 + tid; i < n1; i += kFinishThreads) sortbuf[i] = kPad;
-  __syncthreads();
   block_sort(sortbuf, n1, xch);
 
   if (few) {
@@ -1974,27 +1973,25 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
     };
     if (E2 <= 64) {
       // The class-max pairs s2buf[0, K) are in order already (keys follow the
-      // stage-1 ranks, and so do the pair indices of equal keys); wave 0
-      // sorts the extras, and every record's row is its index plus the
-      // records of the other list below it.
-      if (tid < 64) {
-        uint32_t e = tid < E2 ? s2buf[K + tid] : kPad;
-        e = bitonic_wave(e, tid);
-        s2buf[K + tid] = e;  // s2buf holds kSortCap + 64 records
-      }
-      __syncthreads();
+      // stage-1 ranks, and so do the pair indices of equal keys).  A record's
+      // row is the records below it: its index among the class-max pairs
+      // plus the extras below it (a count over the few extras), or, for an
+      // extra, the extras below it plus the class-max pairs below it (a
+      // binary search).
       const uint32_t* ext = s2buf + K;
       for (uint32_t i = tid; i < K + E2; i += kFinishThreads) {
         const uint32_t rec = s2buf[i];
-        const bool cm = i < K;
-        const uint32_t* other = cm ? ext : s2buf;
-        uint32_t lo = 0, hi = cm ? E2 : K;  // records of the other list below rec
-        while (lo < hi) {
-          const uint32_t mid = (lo + hi) >> 1;
-          if (other[mid] < rec) lo = mid + 1;
-          else hi = mid;
+        uint32_t row = i < K ? i : 0u;
+        for (uint32_t j = 0; j < E2; ++j) row += ext[j] < rec;
+        if (i >= K) {
+          uint32_t lo = 0, hi = K;
+          while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (s2buf[mid] < rec) lo = mid + 1;
+            else hi = mid;
+          }
+          row += lo;
         }
-        const uint32_t row = (cm ? i : i - K) + lo;
         if (row < K) emit(row, rec);
       }
       return;
