@@ -113,6 +113,35 @@ def test_narrowed_blocked_views(gpu, dtype):
                 check(got, ew.binary(op, xc, yc), 0, f"{label} {h}x{w} op{op}")
 
 
+
+@pytest.mark.parametrize("n,c1,h,w", [(2, 8, 20, 20), (1, 16, 40, 40), (3, 4, 7, 9), (2, 130, 2, 2), (1, 1, 1, 1)])
+def test_channel_broadcast_blocked(gpu, n, c1, h, w):
+    """aten add / sub / mul / div of an NC1HWC0 fp16 tensor and a per-channel
+    [1,C1,1,1,16] operand (ops.cpp:464-497), full and C2f-narrowed
+    (x[:, C1/2:]) views, both operand orders and alpha: the flat per-channel
+    kernel (C1 <= 128) and the generic map path beyond it give the oracle's
+    bits, specials included."""
+    from thintnpu_amd import capi
+    g = gen(4000 + n * 131 + c1)
+    x = torch.randn(n, c1, h, w, 16, generator=g).half()
+    flat = x.view(-1)
+    sp = specials16()
+    flat[: min(flat.numel(), sp.numel())] = sp[: flat.numel()]
+    s = (torch.randn(1, c1, 1, 1, 16, generator=g) * 2).half()
+    s.view(-1)[:3] = torch.tensor([0.0, float("inf"), float("nan")]).half()
+    xd, sd = x.to(gpu), s.to(gpu)
+    views = [("full", lambda t: t)]
+    if c1 > 1:
+        views.append(("narrowed", lambda t: t[:, c1 // 2:]))
+    for label, view in views:
+        xc, sc_, xg, sg = view(x), view(s), view(xd), view(sd)
+        for op in (0, 1, 2, 3):
+            for alpha in ((1.0, 0.3) if op in (0, 1) else (1.0,)):
+                got = capi.binary(op, xg, sg, alpha).cpu()
+                check(got, ew.binary(op, xc, sc_.expand_as(xc), alpha), 0, f"{label} x op s op{op} a{alpha}")
+                got = capi.binary(op, sg, xg, alpha).cpu()
+                check(got, ew.binary(op, sc_.expand_as(xc), xc, alpha), 0, f"{label} s op x op{op} a{alpha}")
+
 def test_scalar_operands(gpu):
     from thintnpu_amd import capi
     x = torch.cat([random_bits16((100_000,), 5), specials16()])

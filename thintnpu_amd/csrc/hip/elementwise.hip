@@ -456,13 +456,31 @@ __global__ __launch_bounds__(kThreads) void affine_silu_flat_kernel(AffineFlatPl
   }
 }
 
-bool try_affine_flat(const thin_desc* x, const thin_desc* sc, const thin_desc* b, const thin_desc* out,
-                     hipStream_t stream) {
+// Geometry of the flat form: x and out NC1HWC0 fp16 with dense planes, the
+// C1 planes of an image contiguous, per-channel operands fixed along N.
+struct FlatGeom {
+  uint32_t total, span, plane_vecs, x_row, o_row, c1;
+  uint32_t grid2, grid1;  // blocks for two / one vector per thread
+  bool nt, gapped;
+};
+
+bool nc1hwc0_dense_plane(const thin_desc* d, int64_t h, int64_t w) {
+  return d->dtype == THIN_F16 && d->rank == 5 && d->sizes[4] == 16 && (h == 1 || d->strides[2] == w * 16) &&
+         (w == 1 || d->strides[3] == 16) && d->strides[4] == 1 && reinterpret_cast<uintptr_t>(d->data) % 16 == 0 &&
+         d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0;
+}
+bool nc1hwc0_per_channel(const thin_desc* d) {
+  return d->dtype == THIN_F16 && d->rank == 5 && d->strides[2] == 0 && d->strides[3] == 0 && d->strides[4] == 1 &&
+         reinterpret_cast<uintptr_t>(d->data) % 16 == 0 && d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0;
+}
+
+bool flat_geom(const thin_desc* x, const thin_desc* out, const thin_desc* const* chan, int nchan, FlatGeom& g) {
   const int64_t n = x->sizes[0], c1 = x->sizes[1];
   const int64_t plane_elems = x->sizes[2] * x->sizes[3] * 16;
   if (c1 > (int64_t)kFlatMaxC1) return false;
   if (c1 > 1 && (x->strides[1] != plane_elems || out->strides[1] != plane_elems)) return false;
-  if (n > 1 && (sc->strides[0] != 0 || b->strides[0] != 0)) return false;
+  for (int k = 0; k < nchan; ++k)
+    if (n > 1 && chan[k]->strides[0] != 0) return false;
   const int64_t plane_vecs = plane_elems / 8;
   const int64_t span = c1 * plane_vecs;
   const int64_t total = n * span;
@@ -471,37 +489,57 @@ bool try_affine_flat(const thin_desc* x, const thin_desc* sc, const thin_desc* b
   if (total >= ((int64_t)1 << 31) || x_row < 0 || o_row < 0 || (n - 1) * x_row + span > lim ||
       (n - 1) * o_row + span > lim)
     return false;
+  g.total = (uint32_t)total;
+  g.span = (uint32_t)span;
+  g.plane_vecs = (uint32_t)plane_vecs;
+  g.x_row = (uint32_t)x_row;
+  g.o_row = (uint32_t)o_row;
+  g.c1 = (uint32_t)c1;
+  g.grid2 = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
+  g.grid1 = (uint32_t)((total + kThreads - 1) / kThreads);
+  g.nt = total * 16 >= kStreamingBytes;
+  // Views with gaps between images (the C2f narrowed x[:, C/2:]) read faster
+  // through cached loads, dense tensors through streaming loads
+  // ([32,64,80,80] view of [32,128,80,80]: 9.07 against 10.64 us; the full
+  // tensor: 17.9 against 18.9 us).
+  g.gapped = x_row != 0 && x_row != span;
+  return true;
+}
+
+// Two vectors per thread, or one when that leaves fewer than 256 blocks (a
+// single small image): then more blocks shorten the launch.  Streaming
+// stores from kStreamingBytes; streaming loads for dense inputs only.
+#define THIN_FLAT_LAUNCH(KERNEL, g, stream, ...)                                                           \
+  do {                                                                                                    \
+    if ((g).nt && (g).gapped)                                                                             \
+      hipLaunchKernelGGL((KERNEL<2, false, true, ##__VA_ARGS__>), dim3((g).grid2), dim3(kThreads), 0, stream, p); \
+    else if ((g).nt)                                                                                      \
+      hipLaunchKernelGGL((KERNEL<2, true, true, ##__VA_ARGS__>), dim3((g).grid2), dim3(kThreads), 0, stream, p);  \
+    else if ((g).grid2 >= 256)                                                                            \
+      hipLaunchKernelGGL((KERNEL<2, false, false, ##__VA_ARGS__>), dim3((g).grid2), dim3(kThreads), 0, stream, p); \
+    else                                                                                                  \
+      hipLaunchKernelGGL((KERNEL<1, false, false, ##__VA_ARGS__>), dim3((g).grid1), dim3(kThreads), 0, stream, p); \
+  } while (0)
+
+bool try_affine_flat(const thin_desc* x, const thin_desc* sc, const thin_desc* b, const thin_desc* out,
+                     hipStream_t stream) {
+  const thin_desc* chan[2] = {sc, b};
+  FlatGeom g;
+  if (!flat_geom(x, out, chan, 2, g)) return false;
   AffineFlatPlan p;
   p.x = static_cast<const h8v*>(x->data);
   p.out = static_cast<h8v*>(out->data);
   p.s = static_cast<const h8v*>(sc->data);
   p.b = static_cast<const h8v*>(b->data);
-  p.total = (uint32_t)total;
-  p.span = FastDiv::make((uint32_t)span);
-  p.plane = FastDiv::make((uint32_t)plane_vecs);
-  p.x_row = (uint32_t)x_row;
-  p.o_row = (uint32_t)o_row;
+  p.total = g.total;
+  p.span = FastDiv::make(g.span);
+  p.plane = FastDiv::make(g.plane_vecs);
+  p.x_row = g.x_row;
+  p.o_row = g.o_row;
   p.s_c1 = (uint32_t)(sc->strides[1] / 8);
   p.b_c1 = (uint32_t)(b->strides[1] / 8);
-  p.c1 = (uint32_t)c1;
-  // Two vectors per thread, or one when that leaves fewer than 256 blocks
-  // (a single small image): then more blocks shorten the launch.
-  const uint32_t grid2 = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
-  const bool nt = total * 16 >= kStreamingBytes;
-  // Views with gaps between images (the C2f narrowed x[:, C/2:]) read faster
-  // through cached loads, dense tensors through streaming loads
-  // ([32,64,80,80] view of [32,128,80,80]: 9.07 against 10.64 us; the full
-  // tensor: 17.9 against 18.9 us).
-  const bool gapped = x_row != 0 && x_row != span;
-  if (nt && gapped)
-    hipLaunchKernelGGL((affine_silu_flat_kernel<2, false, true>), dim3(grid2), dim3(kThreads), 0, stream, p);
-  else if (nt)
-    hipLaunchKernelGGL((affine_silu_flat_kernel<2, true, true>), dim3(grid2), dim3(kThreads), 0, stream, p);
-  else if (grid2 >= 256)
-    hipLaunchKernelGGL((affine_silu_flat_kernel<2, false, false>), dim3(grid2), dim3(kThreads), 0, stream, p);
-  else
-    hipLaunchKernelGGL((affine_silu_flat_kernel<1, false, false>), dim3((uint32_t)((total + kThreads - 1) / kThreads)),
-                       dim3(kThreads), 0, stream, p);
+  p.c1 = g.c1;
+  THIN_FLAT_LAUNCH(affine_silu_flat_kernel, g, stream);
   return true;
 }
 
@@ -510,15 +548,9 @@ bool try_affine_blocked(const thin_desc* x, const thin_desc* sc, const thin_desc
                         const thin_desc* out, hipStream_t stream) {
   if (x->dtype != THIN_F16 || x->rank != 5 || x->sizes[4] != 16) return false;
   const int64_t h = x->sizes[2], w = x->sizes[3];
-  auto dense_plane = [&](const thin_desc* d) {
-    return (h == 1 || d->strides[2] == w * 16) && (w == 1 || d->strides[3] == 16) && d->strides[4] == 1 &&
-           reinterpret_cast<uintptr_t>(d->data) % 16 == 0 && d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0;
-  };
-  auto per_channel = [&](const thin_desc* d) {
-    return d->strides[2] == 0 && d->strides[3] == 0 && d->strides[4] == 1 &&
-           reinterpret_cast<uintptr_t>(d->data) % 16 == 0 && d->strides[0] % 8 == 0 && d->strides[1] % 8 == 0;
-  };
-  if (!dense_plane(x) || !dense_plane(out) || !per_channel(sc) || !per_channel(b)) return false;
+  if (!nc1hwc0_dense_plane(x, h, w) || !nc1hwc0_dense_plane(out, h, w) || !nc1hwc0_per_channel(sc) ||
+      !nc1hwc0_per_channel(b))
+    return false;
   if (try_affine_flat(x, sc, b, out, stream)) return true;
   const int64_t planes = x->sizes[0] * x->sizes[1];
   const int64_t plane_vecs = h * w * 2;
@@ -546,6 +578,88 @@ bool try_affine_blocked(const thin_desc* x, const thin_desc* sc, const thin_desc
     if (nt) hipLaunchKernelGGL((affine_silu_blocked_kernel<1, true>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
     else hipLaunchKernelGGL((affine_silu_blocked_kernel<1, false>), dim3(gx, gy), dim3(kThreads), 0, stream, p);
   }
+  return true;
+}
+
+// Per-channel binary op on NC1HWC0 fp16 (aten add / sub / mul / div of a
+// tensor and a [.,C1,1,1,16] operand, in either order) in the flat form of
+// affine_silu_flat_kernel: one vector index decomposition, the image's 2 * C1
+// channel vectors staged once per block in LDS.  Every element goes through
+// the same functor as the generic map kernels, so the bits are theirs.
+struct ChannelFlatPlan {
+  const h8v* x;
+  h8v* out;
+  const h8v* s;      // channel 0, C0 lanes 0-7; lanes 8-15 follow
+  uint32_t total;
+  FastDiv span;
+  FastDiv plane;
+  uint32_t x_row, o_row;
+  uint32_t s_c1;
+  uint32_t c1;
+  float alpha;
+};
+
+template <int U, bool NTL, bool NTS, bool SFIRST, class Op>
+__global__ __launch_bounds__(kThreads) void channel_binary_flat_kernel(ChannelFlatPlan p) {
+  __shared__ h8v sv[2 * kFlatMaxC1];
+  const uint32_t tile = blockIdx.x * (kThreads * U);
+  h8v v[U];
+  uint32_t oo[U], q[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tile + u * kThreads + threadIdx.x;
+    if (i < p.total) {
+      const uint32_t row = p.span.div(i);
+      const uint32_t col = i - row * p.span.d;
+      oo[u] = row * p.o_row + col;
+      q[u] = p.plane.div(col) * 2 + (col & 1u);
+      const h8v* src = p.x + row * p.x_row + col;
+      v[u] = NTL ? __builtin_nontemporal_load(src) : *src;
+    }
+  }
+  for (uint32_t i = threadIdx.x; i < 2 * p.c1; i += kThreads) sv[i] = p.s[(i >> 1) * p.s_c1 + (i & 1u)];
+  __syncthreads();
+  const Op op;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tile + u * kThreads + threadIdx.x;
+    if (i >= p.total) break;
+    const h8v c = sv[q[u]];
+    h8v r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const _Float16 lane[2] = {SFIRST ? c[j] : v[u][j], SFIRST ? v[u][j] : c[j]};
+      r[j] = op.template operator()<_Float16, 2>(lane, p.alpha, 0.f);
+    }
+    store16<NTS>(p.out + oo[u], r);
+  }
+}
+
+template <class Op>
+bool try_channel_flat(const thin_desc* x, const thin_desc* y, const thin_desc* out, float alpha, hipStream_t stream) {
+  if (out->dtype != THIN_F16 || out->rank != 5 || out->sizes[4] != 16) return false;
+  const int64_t h = out->sizes[2], w = out->sizes[3];
+  if (!nc1hwc0_dense_plane(out, h, w)) return false;
+  const bool sfirst = nc1hwc0_per_channel(x) && nc1hwc0_dense_plane(y, h, w);
+  if (!sfirst && !(nc1hwc0_dense_plane(x, h, w) && nc1hwc0_per_channel(y))) return false;
+  const thin_desc* t = sfirst ? y : x;
+  const thin_desc* c = sfirst ? x : y;
+  FlatGeom g;
+  if (!flat_geom(t, out, &c, 1, g)) return false;
+  ChannelFlatPlan p;
+  p.x = static_cast<const h8v*>(t->data);
+  p.out = static_cast<h8v*>(out->data);
+  p.s = static_cast<const h8v*>(c->data);
+  p.total = g.total;
+  p.span = FastDiv::make(g.span);
+  p.plane = FastDiv::make(g.plane_vecs);
+  p.x_row = g.x_row;
+  p.o_row = g.o_row;
+  p.s_c1 = (uint32_t)(c->strides[1] / 8);
+  p.c1 = g.c1;
+  p.alpha = alpha;
+  if (sfirst) THIN_FLAT_LAUNCH(channel_binary_flat_kernel, g, stream, true, Op);
+  else THIN_FLAT_LAUNCH(channel_binary_flat_kernel, g, stream, false, Op);
   return true;
 }
 
@@ -940,6 +1054,19 @@ extern "C" thin_status thin_binary(int32_t op, const thin_desc* x, const thin_de
   const thin_desc* ins[2] = {x, y};
   // PyTorch CPU rounds alpha to the tensor dtype before its fp32 evaluation.
   const float a = round_to(out->dtype, alpha);
+  if (numel(out) != 0) {
+    bool flat = false;
+    switch (op) {
+      case THIN_ADD: flat = try_channel_flat<OpAdd>(x, y, out, a, stream); break;
+      case THIN_SUB: flat = try_channel_flat<OpSub>(x, y, out, a, stream); break;
+      case THIN_MUL: flat = try_channel_flat<OpMul>(x, y, out, 1.f, stream); break;
+      case THIN_DIV: flat = try_channel_flat<OpDiv>(x, y, out, 1.f, stream); break;
+    }
+    if (flat) {
+      THIN_LAUNCH_CHECK("binary_channel_flat");
+      return THIN_OK;
+    }
+  }
   switch (op) {
     case THIN_ADD: return dispatch_float<OpAdd, 2>(out, ins, a, 0.f, stream);
     case THIN_SUB: return dispatch_float<OpSub, 2>(out, ins, a, 0.f, stream);
