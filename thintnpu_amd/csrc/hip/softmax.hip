@@ -526,6 +526,11 @@ struct DecodePlan {
 
 __device__ __forceinline__ _Float16 h_from_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
+// Score vectors per thread: two for the 16-byte form (as the other streaming
+// kernels, which measured best with two), one element otherwise.
+template <int VS>
+constexpr uint32_t kDecodeScoreUnits = VS == 8 ? 2u : 1u;
+
 // LOAD 0: 64-bit pointers.  LOAD 1/2: box offsets fit 32 bits and the bins
 // are read through a buffer resource; 2 also streams the score loads and the
 // output stores (launches of at least kStreamingBytes).
@@ -607,23 +612,39 @@ __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
     }
     return;
   }
-  const uint32_t v = (blockIdx.x - p.box_blocks) * kThreads + threadIdx.x;
-  if (v >= p.score_units) return;
-  const uint32_t row = p.div_svecs.div(v);               // b * nc + c
-  const uint32_t a0 = (v - row * p.svecs) * VS;
-  const uint32_t b = p.div_nc.div(row), c = row - b * p.nc;
-  const _Float16* sp = p.scores + b * p.sb + (int64_t)c * p.sc + (int64_t)a0 * p.sa;
-  _Float16* op = p.out + b * p.ob + (int64_t)(4 + c) * p.oc + (int64_t)a0 * p.oa;
-  if constexpr (VS == 8) {
-    const dev::h8* src = reinterpret_cast<const dev::h8*>(sp);
-    const dev::h8 x = LOAD == 2 ? __builtin_nontemporal_load(src) : *src;
-    dev::h8 y;
+  // scores: two 16-byte vectors per thread (both loads issued first), or one
+  // element per thread in the unaligned form
+  constexpr uint32_t SU = kDecodeScoreUnits<VS>;
+  const uint32_t v0 = (blockIdx.x - p.box_blocks) * (kThreads * SU) + threadIdx.x;
+  const _Float16* sp[SU];
+  _Float16* op[SU];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = (_Float16)dev::sigmoid_fast((float)x[j]);
-    if constexpr (LOAD == 2) __builtin_nontemporal_store(y, reinterpret_cast<dev::h8*>(op));
-    else *reinterpret_cast<dev::h8*>(op) = y;
+  for (uint32_t s = 0; s < SU; ++s) {
+    const uint32_t v = min(v0 + s * kThreads, p.score_units - 1);
+    const uint32_t row = p.div_svecs.div(v);               // b * nc + c
+    const uint32_t a0 = (v - row * p.svecs) * VS;
+    const uint32_t b = p.div_nc.div(row), c = row - b * p.nc;
+    sp[s] = p.scores + b * p.sb + (int64_t)c * p.sc + (int64_t)a0 * p.sa;
+    op[s] = p.out + b * p.ob + (int64_t)(4 + c) * p.oc + (int64_t)a0 * p.oa;
+  }
+  if constexpr (VS == 8) {
+    dev::h8 x[SU];
+#pragma unroll
+    for (uint32_t s = 0; s < SU; ++s) {
+      const dev::h8* src = reinterpret_cast<const dev::h8*>(sp[s]);
+      x[s] = LOAD == 2 ? __builtin_nontemporal_load(src) : *src;
+    }
+#pragma unroll
+    for (uint32_t s = 0; s < SU; ++s) {
+      if (v0 + s * kThreads >= p.score_units) break;
+      dev::h8 y;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (_Float16)dev::sigmoid_fast((float)x[s][j]);
+      if constexpr (LOAD == 2) __builtin_nontemporal_store(y, reinterpret_cast<dev::h8*>(op[s]));
+      else *reinterpret_cast<dev::h8*>(op[s]) = y;
+    }
   } else {
-    op[0] = (_Float16)dev::sigmoid_fast((float)sp[0]);
+    if (v0 < p.score_units) op[0][0] = (_Float16)dev::sigmoid_fast((float)sp[0][0]);
   }
 }
 
@@ -952,7 +973,8 @@ extern "C" thin_status thin_detect_decode(const thin_desc* boxes, const thin_des
   p.div_apairs = FastDiv::make(p.apairs);
   p.div_svecs = FastDiv::make(p.svecs);
   p.div_nc = FastDiv::make((uint32_t)nc);
-  const uint32_t grid = p.box_blocks + (uint32_t)((score_units + kThreads - 1) / kThreads);
+  const uint32_t su = vs ? kDecodeScoreUnits<8> : kDecodeScoreUnits<1>;
+  const uint32_t grid = p.box_blocks + (uint32_t)((score_units + kThreads * su - 1) / (kThreads * su));
   // 32-bit box offsets (buffer loads) when boxes lie within 4 GiB of their base
   bool o32 = true;
   uint64_t extent = 2;
