@@ -118,3 +118,17 @@ def _pair_case(kind, seed):
 def test_selection_pair_paths(gpu, kind, max_det, layout):
     x = _pair_case(kind, 31)
     run_case(gpu, x, max_det, False, layout, f"{kind}-{layout}")
+
+
+@pytest.mark.parametrize("layout", ["transposed", "contiguous"])
+@pytest.mark.parametrize("agnostic,max_det", [(False, 300), (True, 300), (False, 1024)])
+def test_selection_every_encoding_two_launch(gpu, layout, agnostic, max_det):
+    """Every fp16 encoding once, as the scores of 16384 anchors x 4 classes
+    (shuffled), through the two-launch selection's class keys in both load
+    forms (16-byte octets of anchors, and one score a lane)."""
+    g = torch.Generator().manual_seed(65536)
+    bits = torch.randperm(65536, generator=g).to(torch.int32).to(torch.int16)
+    scores = bits.view(torch.float16).reshape(1, 16384, 4)
+    boxes = torch.randn(1, 16384, 4, generator=g).half()
+    x = torch.cat((boxes, scores), -1)
+    run_case(gpu, x, max_det, agnostic, layout, f"every-encoding-{layout}-{agnostic}-{max_det}")

@@ -1319,9 +1319,9 @@ __device__ __forceinline__ uint32_t umed3(uint32_t a, uint32_t b, uint32_t c) {
 }
 __device__ __forceinline__ uint32_t half_of(const u4v& v, uint32_t i) { return (v[i / 2] >> (16 * (i & 1))) & 0xffffu; }
 // Key 0 (NaN) and 0x7fff (zero) stand for several encodings; every other
-// key is one fp16 encoding, score_key's inverse.
+// key is one fp16 encoding, run_key's inverse.
 __device__ __forceinline__ bool key_ambiguous(uint32_t k) { return k == 0u || k == 0x7fffu; }
-__device__ __forceinline__ uint32_t key_bits(uint32_t k) { return k > 0x7fffu ? k : 0x7fffu - k; }
+__device__ __forceinline__ uint32_t key_bits(uint32_t k) { return k > 0x7fffu ? k + 1u : 0x7fffu - k; }
 
 // One bitonic exchange with the lane J away (J < 64): the lower lane of the
 // pair keeps the minimum when `up`, the maximum otherwise.  Whole waves only.
@@ -1530,6 +1530,32 @@ __device__ uint32_t radix_select(Visit visit, uint32_t K, uint32_t* hist, uint32
   return prefix;
 }
 
+// The two-launch selection's key: score_key's order (NaN first, then
+// descending value, +0 and -0 equal) as 0x7fff - |h| for positive h and
+// 0x7fff + |h| for negative h, NaN -> 0.  It differs from score_key only in
+// its values for negative scores (one less), which never meet score_key's:
+// every key of this path comes from run_key / run_key2 and turns back into
+// bits through key_bits.
+__device__ __forceinline__ uint32_t run_key(uint32_t h) {
+  const uint32_t m = h & 0x7fffu;
+  if (m > 0x7c00u) return 0u;
+  return (h & 0x8000u) ? 0x7fffu + m : 0x7fffu - m;
+}
+// run_key of both fp16 halves of w at once (16-bit packed arithmetic).
+__device__ __forceinline__ uint32_t run_key2(uint32_t w) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  typedef short i16x2 __attribute__((ext_vector_type(2)));
+  const uint32_t m = w & 0x7fff7fffu;
+  const u16x2 mv = __builtin_bit_cast(u16x2, m);
+  const uint32_t pos = m ^ 0x7fff7fffu;  // 0x7fff - |h|
+  const uint32_t neg = __builtin_bit_cast(uint32_t, mv + (u16x2)0x7fff);
+  const uint32_t sign = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, w) >> (i16x2)15);
+  const uint32_t key = (neg & sign) | (pos & ~sign);
+  // |h| - 0x7c01 is negative exactly for the non-NaN halves
+  const i16x2 t = __builtin_bit_cast(i16x2, m) - (i16x2)0x7c01;
+  return key & __builtin_bit_cast(uint32_t, t >> (i16x2)15);
+}
+
 // Folds (key << 16 | class) k of a later class, score bits h, into the three
 // smallest so far (b < s < t; kPad where missing): every key is distinct, so
 // the new third is the middle of (s, k, t) and the new second the middle of
@@ -1593,9 +1619,10 @@ __global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
           const uint32_t c = c0 + u * kVGroups;
           if (c < p.nc) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const uint32_t h = half_of(v[u], j);
-              fold3(kb[j], ks[j], kt[j], bits[j], (score_key(h) << 16) | c, h);
+            for (int q = 0; q < 4; ++q) {  // two anchors per 32-bit word
+              const uint32_t w = v[u][q], kw = run_key2(w);
+              fold3(kb[2 * q], ks[2 * q], kt[2 * q], bits[2 * q], (kw << 16) | c, w & 0xffffu);
+              fold3(kb[2 * q + 1], ks[2 * q + 1], kt[2 * q + 1], bits[2 * q + 1], (kw & 0xffff0000u) | c, w >> 16);
             }
           }
         }
@@ -1633,7 +1660,7 @@ __global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
 #pragma unroll
         for (uint32_t u = 0; u < kUnroll; ++u) {
           const uint32_t c = c0 + u * kGroups;
-          if (c < p.nc) fold3(kb, ks, kt, bb, (score_key(bits[u]) << 16) | c, bits[u]);
+          if (c < p.nc) fold3(kb, ks, kt, bb, (run_key(bits[u]) << 16) | c, bits[u]);
         }
       }
       box[grp * kRun + local] = (uint16_t)bxv;
@@ -1949,7 +1976,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
         const uint32_t r = xrank[e];
         const uint32_t x = min((uint32_t)x1[r], kMaxX - 1);
         if (cls != half_of(info1[r], 5)) {
-          const uint32_t key = score_key(xtable[x * nc + cls]);
+          const uint32_t key = run_key(xtable[x * nc + cls]);
           if (key <= T1) {
             const uint32_t slot = atomicAdd(&count2, 1u);
             if (K + slot < kSortCap + 64) s2buf[K + slot] = (key << 16) | (r * nc + cls);
@@ -2025,7 +2052,7 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
           const uint32_t f = r * nc + cls;
           table[f] = (uint16_t)h[u];
           if (p.tr.gathered) static_cast<uint16_t*>(p.tr.gathered)[(size_t)b * K * nc + f] = (uint16_t)h[u];
-          const uint32_t key = score_key(h[u]);
+          const uint32_t key = run_key(h[u]);
           if (key <= T1) {
             const uint32_t slot = atomicAdd(&count, 1u);
             if (slot < kSortCap) s2buf[slot] = (key << 16) | f;
@@ -2046,11 +2073,11 @@ __global__ __launch_bounds__(kFinishThreads) void finish_kernel(RunsPlan p) {
     if (tid == 0) count2 = 0;
     const uint32_t T = radix_select(
         [&](auto&& f) {
-          for (uint32_t i = tid; i < total; i += kFinishThreads) f((score_key(table[i]) << 16) | i);
+          for (uint32_t i = tid; i < total; i += kFinishThreads) f((run_key(table[i]) << 16) | i);
         },
         K, hist, sel);
     for (uint32_t i = tid; i < total; i += kFinishThreads) {
-      const uint32_t rec = (score_key(table[i]) << 16) | i;
+      const uint32_t rec = (run_key(table[i]) << 16) | i;
       if (rec <= T) {
         const uint32_t slot = atomicAdd(&count2, 1u);
         if (slot < kSortCap) s2buf[slot] = rec;  // exactly K
