@@ -120,15 +120,28 @@ def test_selection_pair_paths(gpu, kind, max_det, layout):
     run_case(gpu, x, max_det, False, layout, f"{kind}-{layout}")
 
 
-@pytest.mark.parametrize("layout", ["transposed", "contiguous"])
+@pytest.mark.parametrize("layout", ["transposed", "contiguous", "strided"])
 @pytest.mark.parametrize("agnostic,max_det", [(False, 300), (True, 300), (False, 1024)])
 def test_selection_every_encoding_two_launch(gpu, layout, agnostic, max_det):
     """Every fp16 encoding once, as the scores of 16384 anchors x 4 classes
-    (shuffled), through the two-launch selection's class keys in both load
-    forms (16-byte octets of anchors, and one score a lane)."""
+    (shuffled), through the two-launch selection's class keys in its three
+    load forms: 16-byte octets of anchors (transposed), 8-byte chunks of a
+    contiguous row, and one score a lane (strided)."""
     g = torch.Generator().manual_seed(65536)
     bits = torch.randperm(65536, generator=g).to(torch.int32).to(torch.int16)
     scores = bits.view(torch.float16).reshape(1, 16384, 4)
     boxes = torch.randn(1, 16384, 4, generator=g).half()
     x = torch.cat((boxes, scores), -1)
     run_case(gpu, x, max_det, agnostic, layout, f"every-encoding-{layout}-{agnostic}-{max_det}")
+
+
+@pytest.mark.parametrize("batch,anchors,nc,max_det", [(2, 129, 4, 100), (2, 257, 12, 300), (3, 1000, 100, 300),
+                                                      (1, 3360, 256, 300), (2, 8400, 80, 300)])
+@pytest.mark.parametrize("agnostic", [False, True])
+def test_selection_row_form(gpu, batch, anchors, nc, max_det, agnostic):
+    """Contiguous rows read as 8-byte class chunks (nc a multiple of 4): a
+    partial last run of anchors, chunk counts not a multiple of the four
+    lanes of an anchor, classes over two load passes, and batches."""
+    from tests.selection_fixtures import predictions
+    x = predictions(batch, anchors, nc, seed=anchors + nc)
+    run_case(gpu, x, max_det, agnostic, "contiguous", f"row-{batch}x{anchors}x{nc}-{agnostic}")

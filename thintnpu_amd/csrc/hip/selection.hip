@@ -1306,6 +1306,7 @@ struct RunsPlan {
   uint32_t rows_per;      // finish: stage-1 ranks per gather pass, kFinishThreads / nc
   int32_t agnostic;
   int32_t vec_classes;    // anchors contiguous in aligned 16-byte groups
+  int32_t row_classes;    // classes contiguous, rows in aligned 8-byte chunks, nc % 4 == 0
   uint32_t* runs_rec;     // [B, runs, kRun]: sorted records
   uint16_t* runs_side;    // [B, runs, kRun]: row key of each record's anchor
   u4v* info;              // [B, A] halves: box[4], class-max bits, class, second key, second class
@@ -1569,10 +1570,10 @@ __device__ __forceinline__ void fold3(uint32_t& b, uint32_t& s, uint32_t& t, uin
   }
 }
 
-// Class keys of kRun anchors (the two load forms of slice_kernel) and their
-// box channels; then the run's records sorted: waves 0 and 1 sort 64 each
-// (ascending, descending), one LDS exchange at distance 64 and the in-wave
-// end of the last merge.
+// Class keys of kRun anchors (the two load forms of slice_kernel, and a row
+// form for rows of contiguous classes) and their box channels; then the
+// run's records sorted: waves 0 and 1 sort 64 each (ascending, descending),
+// one LDS exchange at distance 64 and the in-wave end of the last merge.
 __global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
   constexpr uint32_t kTiles = kRun / 64;                  // scalar form: 64-anchor tiles
   constexpr uint32_t kGroups = kRunThreads / kRun;        // scalar form: class groups per anchor
@@ -1580,6 +1581,8 @@ __global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
   constexpr uint32_t kOctets = kRun / 8;
   constexpr uint32_t kVGroups = kRunThreads / kOctets;    // vector form: class groups per octet
   constexpr uint32_t kVUnroll = 4;                        // vector form: 16-byte loads in flight per lane
+  constexpr uint32_t kRUnroll = 6;                        // row form: 8-byte loads in flight per lane
+  static_assert(kRunThreads == 4 * kRun, "row form: four lanes per anchor");
   constexpr uint32_t kParts = kRunThreads / kRun;         // group-reduction parts per anchor
   static_assert(kVGroups == kParts * 8 && kGroups == kParts && kGroups == 4, "group reduction shape");
   // per class group and anchor: the three smallest (key << 16 | class), best bits
@@ -1639,6 +1642,57 @@ __global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
       g_s[at] = ks[j];
       g_t[at] = kt[j];
       g_bits[at] = (uint16_t)bits[j];
+    }
+  } else if (p.row_classes) {
+    // four lanes per anchor: lane g reads the anchor's 8-byte class chunks g,
+    // g + 4, ... (lane 0 also the box chunk before them), then the quad merges
+    // its four triples in two exchanges, leaving the anchor's three in every lane
+    typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+    const uint32_t local = tid / 4u, g = tid % 4u, a = run * kRun + local, nch = p.nc / 4u;
+    uint32_t kb = kPad, ks = kPad, kt = kPad, bb = 0u;
+    u2v bx = (u2v)0u;
+    if (a < p.A) {
+      // one image spans fewer than 2^31 elements (checked on the host)
+      const u2v* row = reinterpret_cast<const u2v*>(img + a * (uint32_t)p.L.sa);
+      if (g == 0) bx = row[0];
+      for (uint32_t j0 = g; j0 < nch; j0 += 4u * kRUnroll) {
+        u2v v[kRUnroll];
+#pragma unroll
+        for (uint32_t u = 0; u < kRUnroll; ++u) {
+          const uint32_t j = j0 + 4u * u;
+          v[u] = j < nch ? row[1u + j] : (u2v)0u;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kRUnroll; ++u) {
+          const uint32_t j = j0 + 4u * u;
+          if (j < nch) {
+#pragma unroll
+            for (uint32_t q = 0; q < 2; ++q) {  // classes 4j + 2q and 4j + 2q + 1
+              const uint32_t w = v[u][q], kw = run_key2(w), c = 4u * j + 2u * q;
+              fold3(kb, ks, kt, bb, (kw << 16) | c, w & 0xffffu);
+              fold3(kb, ks, kt, bb, (kw & 0xffff0000u) | (c + 1u), w >> 16);
+            }
+          }
+        }
+      }
+    }
+    auto merge = [&](uint32_t pb, uint32_t ps, uint32_t pt, uint32_t ph) {
+      uint32_t unused = 0;
+      fold3(kb, ks, kt, bb, pb, ph);
+      fold3(kb, ks, kt, unused, ps, 0u);  // never below the partner's best, so bits stay
+      fold3(kb, ks, kt, unused, pt, 0u);
+    };
+    merge(dev::lane_xor_bits<1>(kb), dev::lane_xor_bits<1>(ks), dev::lane_xor_bits<1>(kt),
+          dev::lane_xor_bits<1>(bb));
+    merge(dev::lane_xor_bits<2>(kb), dev::lane_xor_bits<2>(ks), dev::lane_xor_bits<2>(kt),
+          dev::lane_xor_bits<2>(bb));
+    if (g == 0) {
+      g_b[local] = kb;
+      g_s[local] = ks;
+      g_t[local] = kt;
+      g_bits[local] = (uint16_t)bb;
+#pragma unroll
+      for (uint32_t c = 0; c < 4; ++c) box[c * kRun + local] = (uint16_t)(bx[c / 2] >> (16 * (c & 1)));
     }
   } else {
     const uint32_t lane = tid & 63u, wave = tid >> 6;
@@ -1711,6 +1765,13 @@ __global__ __launch_bounds__(kRunThreads) void runs_kernel(RunsPlan p) {
     if (tid < kRun)
       reduce(part_b + tid, part_s + tid, part_t + tid, part_bits + tid, std::integral_constant<uint32_t, kParts>(), 0u,
              kb, ks, kt, bb);
+  } else if (p.row_classes) {
+    if (tid < kRun) {
+      kb = g_b[tid];
+      ks = g_s[tid];
+      kt = g_t[tid];
+      bb = g_bits[tid];
+    }
   } else if (tid < kRun) {
     reduce(g_b + tid, g_s + tid, g_t + tid, g_bits + tid, std::integral_constant<uint32_t, kGroups>(), 0u, kb, ks, kt,
            bb);
@@ -2319,6 +2380,11 @@ thin_status select_run(const thin_desc* decoded, int64_t max_det, bool agn, void
     rp.rows_per = w.two.rows_per;
     rp.agnostic = agn ? 1 : 0;
     rp.vec_classes = vec_classes ? 1 : 0;
+    rp.row_classes = !vec_classes && decoded->strides[2] == 1 && decoded->strides[1] % 4 == 0 && nc % 4 == 0 &&
+                             (B == 1 || decoded->strides[0] % 4 == 0) &&
+                             reinterpret_cast<uintptr_t>(decoded->data) % 8 == 0
+                         ? 1
+                         : 0;
     rp.runs_rec = reinterpret_cast<uint32_t*>(ws + w.runs);
     rp.runs_side = reinterpret_cast<uint16_t*>(ws + w.runs_side);
     rp.info = reinterpret_cast<u4v*>(ws + w.info);
