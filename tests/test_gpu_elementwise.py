@@ -324,12 +324,13 @@ def test_errors_are_reported(gpu):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.int32, torch.bfloat16])
 def test_transpose_copy(gpu, dtype):
     """Batched 2-D transposes take the tiled path: full and partial tiles,
-    aligned and misaligned rows, NCHW <-> NHWC permutes; bit-exact."""
+    several tile rows and batches, aligned and misaligned rows, NCHW <-> NHWC
+    permutes; bit-exact."""
     from thintnpu_amd import capi
     g = gen(5)
     raw = torch.randint(-2 ** 31, 2 ** 31 - 1, (3, 130, 1040), generator=g, dtype=torch.int64).to(torch.int32)
     base = raw.view(dtype) if dtype.itemsize == 4 else raw.view(torch.int16).view(dtype)[..., :1040]
-    for shape in ((2, 64, 6400), (1, 130, 257), (3, 17, 1000), (1, 64, 64), (2, 100, 16)):
+    for shape in ((2, 64, 6400), (3, 128, 1024), (1, 130, 257), (3, 17, 1000), (1, 64, 64), (2, 100, 16)):
         b, m, n = shape
         x = base[:b, :m, :n]
         for offset in (0, 1):
