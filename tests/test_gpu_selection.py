@@ -145,3 +145,40 @@ def test_selection_row_form(gpu, batch, anchors, nc, max_det, agnostic):
     from tests.selection_fixtures import predictions
     x = predictions(batch, anchors, nc, seed=anchors + nc)
     run_case(gpu, x, max_det, agnostic, "contiguous", f"row-{batch}x{anchors}x{nc}-{agnostic}")
+
+
+@pytest.mark.parametrize("noalloc", [False, True])
+def test_selection_graph_replays(gpu, noalloc):
+    """Selections captured into a HIP graph: every replay, with eager
+    selections on the same device between replays, gives the eager result
+    bit for bit, on the C5 image (transposed view) and a 4-image batch, with
+    a workspace and on the static scratch."""
+    from thintnpu_amd import capi
+    from tests.selection_fixtures import predictions
+    cases = []
+    for x, layout, k in ((c5_selection_input(), "transposed", 300), (predictions(4, 3360, 80, seed=78), "contiguous", 300)):
+        base, view = backing_and_view(x, layout)
+        dv = view(base.to(gpu))
+        ref = sel.select(view(base), k, False)["output"]
+        eager = capi.detection_select(dv, k, noalloc=noalloc)
+        assert bits_equal(eager.cpu(), ref)
+        cases.append((dv, k, eager))
+    outs = [torch.full_like(e, float("nan")) for _, _, e in cases]
+    wss = [None if noalloc else torch.empty(capi.detection_select_workspace(dv.shape[0], dv.shape[1], dv.shape[2] - 4,
+                                                                            k, False), dtype=torch.uint8, device=gpu)
+           for dv, k, _ in cases]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for (dv, k, _), o, ws in zip(cases, outs, wss):
+            capi.detection_select(dv, k, out=o, workspace=ws, noalloc=noalloc)
+    for replay in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for (dv, k, eager), o in zip(cases, outs):
+            assert bits_equal(o.cpu(), eager.cpu()), f"replay {replay}"
+        # eager calls between replays
+        for dv, k, eager in cases:
+            assert bits_equal(capi.detection_select(dv, k, noalloc=noalloc).cpu(), eager.cpu())
