@@ -136,12 +136,14 @@ def test_selection_every_encoding_two_launch(gpu, layout, agnostic, max_det):
 
 
 @pytest.mark.parametrize("batch,anchors,nc,max_det", [(2, 129, 4, 100), (2, 257, 12, 300), (3, 1000, 100, 300),
-                                                      (1, 3360, 256, 300), (2, 8400, 80, 300)])
+                                                      (1, 3360, 256, 300), (2, 8400, 80, 300), (1, 1, 4, 300),
+                                                      (3, 7, 8, 5), (1, 500, 1024, 32)])
 @pytest.mark.parametrize("agnostic", [False, True])
 def test_selection_row_form(gpu, batch, anchors, nc, max_det, agnostic):
     """Contiguous rows read as 8-byte class chunks (nc a multiple of 4): a
     partial last run of anchors, chunk counts not a multiple of the four
-    lanes of an anchor, classes over two load passes, and batches."""
+    lanes of an anchor, classes over two or more load passes (up to the
+    1024-class maximum), single- and few-anchor images, and batches."""
     from tests.selection_fixtures import predictions
     x = predictions(batch, anchors, nc, seed=anchors + nc)
     run_case(gpu, x, max_det, agnostic, "contiguous", f"row-{batch}x{anchors}x{nc}-{agnostic}")
