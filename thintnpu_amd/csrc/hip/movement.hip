@@ -787,7 +787,7 @@ __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
 #pragma unroll
         for (int dy = 0; dy <= 2 * R; ++dy) keep_max(m, hm[(r + dy) * row_vecs + k]);
       }
-      in[(r + R) * prow + k + VPP * R] = m;  // the next repeat's input
+      if (rep < p.repeats) in[(r + R) * prow + k + VPP * R] = m;  // the next repeat's input
       const h8 hv = __builtin_bit_cast(h8, m);
       h8* dst = reinterpret_cast<h8*>(yr + (int64_t)r * p.ys[2] + (int64_t)(k / VPP) * 16 + (VPP == 2 ? (k & 1u) * 8 : 0u));
       if constexpr (NT) __builtin_nontemporal_store(hv, dst);
