@@ -180,6 +180,42 @@ def test_unary_in_place_on_strided_parent(gpu):
     assert_ulp(x.cpu(), ref, 2, "silu_ in place")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_row_views(gpu, dtype):
+    """Operands that coalesce to rows of contiguous vectors with their own row
+    strides (narrowed NC1HWC0 halves, column slices, a row broadcast), in
+    place and into dense outputs: unary, binary and copy against the oracle."""
+    from thintnpu_amd import capi
+    g = gen(4242)
+    parent = torch.randn(3, 8, 7, 9, 16, generator=g).to(dtype)
+    other = torch.randn(3, 8, 7, 9, 16, generator=g).to(dtype)
+    pd, od = parent.to(gpu), other.to(gpu)
+    halves = [(lambda t: t[:, 4:]), (lambda t: t[:, :4]), (lambda t: t[:, 2:6])]
+    for k, view in enumerate(halves):
+        xc, xg = view(parent), view(pd)
+        for op, ref in ((capi.SIGMOID, ew.sigmoid), (capi.SILU, ew.silu)):
+            check(capi.unary(op, xg).cpu(), ref(xc), 2, f"unary{op} view{k}")
+        for op in (0, 1, 2, 3):
+            check(capi.binary(op, xg, view(od)).cpu(), ew.binary(op, xc, view(other)), 0, f"binary{op} view{k}")
+            check(capi.binary(op, xg, od[:, :4]).cpu(), ew.binary(op, xc, other[:, :4]), 0, f"binary{op} mixed{k}")
+        dense = torch.empty(xg.shape, dtype=dtype, device=gpu)
+        capi.copy(xg, dense)
+        assert torch.equal(dense.cpu().view(torch.uint8), xc.contiguous().view(torch.uint8)), f"copy view{k}"
+    # in place on a narrowed half: the rest of the parent stays as it was
+    work = pd.clone()
+    capi.unary(capi.SILU, work[:, 4:], out=work[:, 4:])
+    expect = parent.clone()
+    expect[:, 4:] = ew.silu(parent[:, 4:])
+    check(work.cpu(), expect, 2, "silu_ in place on a half")
+    # column slices of a matrix and a broadcast row
+    mat = torch.randn(40, 272, generator=g).to(dtype)
+    row = torch.randn(1, 128, generator=g).to(dtype)
+    md, rd = mat.to(gpu), row.to(gpu)
+    for op in (0, 1, 2, 3):
+        check(capi.binary(op, md[:, 8:136], rd).cpu(), ew.binary(op, mat[:, 8:136], row), 0, f"binary{op} row")
+        check(capi.binary(op, rd, md[:, 136:264]).cpu(), ew.binary(op, row, mat[:, 136:264]), 0, f"binary{op} row first")
+
+
 # C1's recorded bar: how many elements (of 1.6 M at N=1, 52 M at N=32) may pass
 # only through the cancellation arm, and how many fp16 ulps apart.  Measured:
 # none at either batch; every element is within 2 ulp (N=32: 52,427,659 of
