@@ -963,58 +963,70 @@ struct TransposePlan {
   uint32_t vec_src, vec_dst; // 16-byte rows possible (alignment checked on the host)
 };
 
-template <typename T, bool NT>
+// W tiles per block along p (W = 2: 2-byte elements, every tile whole and
+// both sides 16-byte aligned, which the host checks): a source row is then
+// read W * 128 contiguous bytes at a time instead of 128.
+template <typename T, bool NT, uint32_t W>
 __global__ __launch_bounds__(kThreads) void transpose_kernel(TransposePlan p) {
+  static_assert(W == 1 || (W == 2 && sizeof(T) == 2), "wide blocks: 2-byte elements only");
   constexpr uint32_t V = 16 / sizeof(T);
   constexpr uint32_t kRow = kTile + 4 / sizeof(T);  // padded LDS row, in elements
-  __shared__ __attribute__((aligned(16))) T tile[kTile * kRow];
-  const uint32_t per_b = p.tiles_m * p.tiles_p;
+  __shared__ __attribute__((aligned(16))) T tile[W * kTile * kRow];
+  const uint32_t tiles_p = p.tiles_p / W;  // blocks along p
+  const uint32_t per_b = p.tiles_m * tiles_p;
   const uint32_t b = blockIdx.x / per_b, rest = blockIdx.x - b * per_b;
-  const uint32_t tm = rest / p.tiles_p, tp = rest - tm * p.tiles_p;
+  const uint32_t tm = rest / tiles_p, tp = (rest - tm * tiles_p) * W;
   const uint32_t m0 = tm * kTile, p0 = tp * kTile;
   const T* src = reinterpret_cast<const T*>(p.src) + b * p.s_b;
   T* dst = reinterpret_cast<T*>(p.dst) + b * p.d_b;
-  const bool full = m0 + kTile <= p.M && p0 + kTile <= p.P;
+  const bool full = m0 + kTile <= p.M && p0 + W * kTile <= p.P;
   if constexpr (sizeof(T) == 2) {
-    if (full && p.vec_src && p.vec_dst) {
+    if (W == 2 || (full && p.vec_src && p.vec_dst)) {
       // whole 2-byte tiles with 16-byte rows on both sides: every load in
       // flight before the LDS writes (4-byte words), and each thread reads
       // 4-byte column pairs from 8 tile rows to build two output vectors
       typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-      constexpr uint32_t U = kTile * kTile / V / kThreads;  // 2
+      constexpr uint32_t CV = W * kTile / V;                // 16-byte vectors per staged row
+      constexpr uint32_t U = W * kTile * kTile / V / kThreads;  // 2 per tile
       constexpr uint32_t kWords = kRow / 2;                 // padded row in 4-byte words (33)
       uint32_t* words = reinterpret_cast<uint32_t*>(tile);
       u32x4_t w[U];
 #pragma unroll
       for (uint32_t u = 0; u < U; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
-        const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+        const uint32_t r = i / CV, cv = (i % CV) * V;
         w[u] = load16<NT, u32x4_t>(src + (int64_t)(m0 + r) * p.s_m + p0 + cv);
       }
 #pragma unroll
       for (uint32_t u = 0; u < U; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
-        const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+        const uint32_t r = i / CV, cv = (i % CV) * V;
+        const uint32_t t = cv / kTile, c = cv % kTile;  // tile of the block, column in it
 #pragma unroll
-        for (uint32_t k = 0; k < 4; ++k) words[r * kWords + cv / 2 + k] = w[u][k];
+        for (uint32_t k = 0; k < 4; ++k) words[(t * kTile + r) * kWords + c / 2 + k] = w[u][k];
       }
       __syncthreads();
       // thread -> (column pair qp of the tile, 8-row group g): lanes 8 apart
       // share a destination row, and the 64 lanes hit 64 distinct banks
       const uint32_t g = threadIdx.x % (kTile / 8), qp = threadIdx.x / (kTile / 8);
-      uint32_t lo[4], hi[4];
 #pragma unroll
-      for (uint32_t j = 0; j < 8; j += 2) {
-        const uint32_t a = words[(g * 8 + j) * kWords + qp], b = words[(g * 8 + j + 1) * kWords + qp];
-        lo[j / 2] = (a & 0xffffu) | (b << 16);           // column 2qp, rows g*8+j, +1
-        hi[j / 2] = (a >> 16) | (b & 0xffff0000u);       // column 2qp+1
+      for (uint32_t t = 0; t < W; ++t) {
+        const uint32_t* tw = words + t * kTile * kWords;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; j += 2) {
+          const uint32_t a = tw[(g * 8 + j) * kWords + qp], b = tw[(g * 8 + j + 1) * kWords + qp];
+          lo[j / 2] = (a & 0xffffu) | (b << 16);           // column 2qp, rows g*8+j, +1
+          hi[j / 2] = (a >> 16) | (b & 0xffff0000u);       // column 2qp+1
+        }
+        T* row0 = dst + (int64_t)(p0 + t * kTile + 2 * qp) * p.d_p + m0 + g * 8;
+        store16<NT>(row0, (u32x4_t){lo[0], lo[1], lo[2], lo[3]});
+        store16<NT>(row0 + p.d_p, (u32x4_t){hi[0], hi[1], hi[2], hi[3]});
       }
-      T* row0 = dst + (int64_t)(p0 + 2 * qp) * p.d_p + m0 + g * 8;
-      store16<NT>(row0, (u32x4_t){lo[0], lo[1], lo[2], lo[3]});
-      store16<NT>(row0 + p.d_p, (u32x4_t){hi[0], hi[1], hi[2], hi[3]});
       return;
     }
   }
+  if constexpr (W == 1) {
   // load: tile row r = m0 + r, columns p0 .. p0+63
   for (uint32_t i = threadIdx.x; i < kTile * kTile / V; i += kThreads) {
     const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
@@ -1044,6 +1056,7 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(TransposePlan p) {
       for (uint32_t j = 0; j < V; ++j)
         if (p0 + q < p.P && m0 + cm + j < p.M) row[j] = w.v[j];
     }
+  }
   }
 }
 
@@ -1076,7 +1089,7 @@ bool try_transpose(const thin_desc* src, const thin_desc* dst, hipStream_t strea
   t.d_b = bd >= 0 ? c.stride[0][bd] : 0;
   t.tiles_m = (uint32_t)((M + kTile - 1) / kTile);
   t.tiles_p = (uint32_t)((P + kTile - 1) / kTile);
-  const uint64_t blocks = (uint64_t)B * t.tiles_m * t.tiles_p;
+  uint64_t blocks = (uint64_t)B * t.tiles_m * t.tiles_p;
   if (M >= (1ll << 31) || P >= (1ll << 31) || blocks >= (1ull << 31)) return false;
   auto a16 = [](const void* q, int64_t stride, int e) {
     return reinterpret_cast<uintptr_t>(q) % 16 == 0 && (stride * e) % 16 == 0;
@@ -1084,14 +1097,21 @@ bool try_transpose(const thin_desc* src, const thin_desc* dst, hipStream_t strea
   t.vec_src = a16(src->data, t.s_m, esz) && (t.s_b * esz) % 16 == 0;
   t.vec_dst = a16(dst->data, t.d_p, esz) && (t.d_b * esz) % 16 == 0;
   const bool nt = (int64_t)B * M * P * esz >= kStreamingBytes;
-  if (esz == 2 && nt)
-    hipLaunchKernelGGL((transpose_kernel<uint16_t, true>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+  // two tiles per block when every tile is whole and 16-byte aligned
+  const bool wide = esz == 2 && M % kTile == 0 && P % (2 * kTile) == 0 && t.vec_src && t.vec_dst;
+  if (wide) blocks /= 2;
+  if (wide && nt)
+    hipLaunchKernelGGL((transpose_kernel<uint16_t, true, 2>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+  else if (wide)
+    hipLaunchKernelGGL((transpose_kernel<uint16_t, false, 2>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+  else if (esz == 2 && nt)
+    hipLaunchKernelGGL((transpose_kernel<uint16_t, true, 1>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
   else if (esz == 2)
-    hipLaunchKernelGGL((transpose_kernel<uint16_t, false>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+    hipLaunchKernelGGL((transpose_kernel<uint16_t, false, 1>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
   else if (nt)
-    hipLaunchKernelGGL((transpose_kernel<uint32_t, true>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+    hipLaunchKernelGGL((transpose_kernel<uint32_t, true, 1>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
   else
-    hipLaunchKernelGGL((transpose_kernel<uint32_t, false>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
+    hipLaunchKernelGGL((transpose_kernel<uint32_t, false, 1>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, t);
   return true;
 }
 
