@@ -15,7 +15,9 @@ Also reported (``ops``): per-op / per-chain µs and GB/s at N=1 (cache-resident
 and rotated) and N=32 for every op built, each beside the reference's CPU path
 (the stock PyTorch CPU op sequence) timed on the host cores, the roofline of
 the dominant kernel, and the CPU path of the step itself (``cpu_baseline``).
-Only rank 0 prints: one JSON line on stdout; progress goes to stderr.
+Only rank 0 prints: one compact JSON line on stdout (the headline, roofline and
+CPU baseline); progress and the per-op rows (one JSON object per line) go to
+stderr.
 """
 from __future__ import annotations
 
@@ -732,6 +734,7 @@ def main():
                          "'copy@<C>x<H>x<W>' (a copy of one N=32 C2 tensor), 'floor' (a one-element fill: "
                          "the per-launch floor), or 'op:<row name>[@N]' for one row of the per-op table "
                          "(N=32 by default, rotated)")
+    ap.add_argument("--ops-json", default=None, help="also write the per-op rows to this file")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the multi-GPU sharding of "
@@ -926,23 +929,44 @@ def main():
                 torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline()
+    # The per-op table goes to stderr, one JSON object per row, and to
+    # --ops-json when given; stdout's last line is the compact headline.
+    for row in ops:
+        log(json.dumps(row))
+    if args.ops_json:
+        Path(args.ops_json).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.ops_json).write_text(json.dumps(ops, indent=1) + "\n")
+    line = headline(value=value, step_s=step_s, steps=args.steps, warmup=args.warmup, batch=n,
+                    launches=len(work), step_bytes=step_bytes, nrot=nrot, roofline=roofline, cpu=cpu,
+                    op_rows=len(ops))
+    print(json.dumps(line), flush=True)
+
+
+HEADLINE_MAX_BYTES = 4096  # the driver reads the tail of stdout; the last line must fit in it whole
+
+
+def headline(*, value, step_s, steps, warmup, batch, launches, step_bytes, nrot, roofline, cpu, op_rows):
+    """The bench's last stdout line: the step's throughput, its roofline and
+    CPU baseline, in a few KB (the per-op rows are printed on stderr)."""
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_s * 1e3, 4),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(step_s * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic",
         "config": {"workload": "affine+SiLU y=SiLU(x*s+b), per-channel [1,C,1,1] broadcast, NC1HWC0 fp16, "
                                "N=32, (C,H,W) in {(128,80,80),(256,40,40),(512,20,20)}, full + C2f "
                                "narrowed view x[:,C/2:]",
-                   "batch": n, "shapes": C2_SHAPES, "launches_per_step": len(work),
+                   "batch": batch, "shapes": C2_SHAPES, "launches_per_step": launches,
                    "algorithmic_bytes_per_step": step_bytes, "rotated_sets": nrot,
                    "steps_per_graph": GRAPH_STEPS},
         "pct_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "ops": ops,
+        "ops_rows": op_rows,
+        "ops_where": "stderr, one JSON object per row (and --ops-json)",
     }
-    print(json.dumps(line), flush=True)
+    assert len(json.dumps(line)) <= HEADLINE_MAX_BYTES, "bench headline line too long"
+    return line
 
 
 if __name__ == "__main__":

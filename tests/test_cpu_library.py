@@ -176,3 +176,23 @@ def test_no_cpu_fallback_without_library(monkeypatch, tmp_path):
     monkeypatch.setattr(capi, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         capi.lib()
+
+
+def test_bench_headline_is_one_short_json_line():
+    """bench.py's last stdout line is the headline alone: it parses as JSON,
+    carries the contract's keys and stays within the size the driver reads
+    whole, however many per-op rows the run measured (those go to stderr)."""
+    import json
+    import bench
+    roofline = {"bound": "hbm", "achieved": 5800.0, "peak": 8000.0, "unit": "GB/s", "frac": 0.725,
+                "traffic": 104882304, "kernel": "k" * 80, "launch": "l" * 120, "traffic_note": "t" * 300}
+    cpu = {"value": 14.1, "unit": "GB/s", "cores": 16, "kind": "port", "sample": "s" * 400}
+    line = bench.headline(value=4974.1, step_s=55.3e-6, steps=50, warmup=10, batch=32, launches=6,
+                          step_bytes=275256576, nrot=3, roofline=roofline, cpu=cpu, op_rows=120)
+    text = json.dumps(line)
+    assert "\n" not in text and len(text) <= bench.HEADLINE_MAX_BYTES
+    parsed = json.loads(text)
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "dtype", "config",
+                "pct_peak", "roofline", "cpu_baseline", "higher_is_better", "scaling", "vs_baseline", "data"):
+        assert key in parsed, key
+    assert "ops" not in parsed and parsed["roofline"]["frac"] == 0.725

@@ -96,3 +96,75 @@ def test_contract_rejects_cpu_and_inference_tensors():
         m.register_buffer("frozen", torch.zeros(2))
     with pytest.raises(ValueError, match="no_grad"):
         RegionContract((m,))
+
+
+def test_drifts_are_reported_in_contract_order():
+    """When several drifts coexist, the first in the contract's order is the
+    one reported: global hooks, then class forwards, then per module its class,
+    __dict__, training, hooks, children, forward, attributes and tensors; and a
+    drift in an earlier module before any drift in a later one."""
+    m = model()
+    g = guard(m)
+    m.train()                                            # every module: training
+    m[0].register_forward_hook(lambda *a: None)          # module 1: hooks
+    with pytest.raises(ValueError, match="Region is inference-only"):
+        g.validate()
+    m.eval()
+    with pytest.raises(ValueError, match="Region hooks changed"):
+        g.validate()
+
+    m = model()
+    g = guard(m)
+    m[2].forward = lambda x: x                           # module 3: forward
+    m[1].inplace = True                                  # module 2: attribute
+    with pytest.raises(ValueError, match="Region operator configuration changed"):
+        g.validate()
+    m[1].inplace = False
+    with pytest.raises(ValueError, match="Region forward changed"):
+        g.validate()
+
+    m = model()
+    g = guard(m)
+    m[0].weight.add_(1)                                  # module 1: tensor version
+    m[0].stride = (2, 2)                                 # module 1: attribute
+    original = nn.Upsample.forward
+    nn.Upsample.forward = lambda self, x: x              # a class forward
+    handle = nn.modules.module.register_module_forward_hook(lambda *a: None)
+    try:
+        with pytest.raises(ValueError, match="Global module hooks are unsupported"):
+            g.validate()
+        handle.remove()
+        with pytest.raises(ValueError, match="Module class forward changed"):
+            g.validate()
+    finally:
+        handle.remove()
+        nn.Upsample.forward = original
+    with pytest.raises(ValueError, match="Region operator configuration changed"):
+        g.validate()
+    m[0].stride = (1, 1)
+    with pytest.raises(ValueError, match="version or gradient mode"):
+        g.validate()
+
+
+def test_construction_errors():
+    """Snapshot-time contract: a non-method forward, a non-tensor slot and a
+    region that requires grad are rejected when the Guard is built."""
+    m = model()
+    m[1].forward = 3                                     # not a bound method
+    with pytest.raises(ValueError, match="Expected a bound module forward"):
+        guard(m)
+    m = model()
+    m[0]._parameters["odd"] = 3
+    with pytest.raises(TypeError, match="Expected a Tensor or None"):
+        guard(m)
+    m = model()
+    m[0].bias.requires_grad_(True)
+    with pytest.raises(ValueError, match="gradient mode"):
+        guard(m)
+    m = model()
+    m[0].bias = None                                     # a None slot is frozen as None
+    g = guard(m)
+    g.validate()
+    m[0].bias = nn.Parameter(torch.zeros(8), requires_grad=False)
+    with pytest.raises(ValueError, match="identity changed"):
+        g.validate()

@@ -224,7 +224,44 @@ def test_frozen_graph(npu):
         y = torch.linspace(0, 1, 4096).half().to(npu)
         assert torch.equal(g(y).cpu(), expression(y).cpu())
         assert Pilot.calls == 3
+        # the reference's surface: .graph is the CapturedForward, and a replay
+        # made through it is validated too
+        from thin_backend.graph import CapturedForward
+        assert isinstance(g.graph, CapturedForward) and g.outputs is g.graph.outputs
+        assert torch.equal(g.graph.replay().cpu(), expression(y).cpu())
+        assert Pilot.calls == 4
         g.close()
+
+
+def test_replays_enqueue_and_stay_ordered(npu):
+    """RuntimeGraph.replay only enqueues (backend.cpp:89-93 in the reference):
+    back-to-back replays of several captured forwards, then one read, equal the
+    eager results; an eager op right after a replay on the same thread reads
+    the replay's outputs; a changed input between replays is honoured."""
+    from thin_backend.graph import CapturedForward
+    with torch.inference_mode():
+        xs = [normal16((2, 8, 20, 20, 16), 900 + i).to(npu) for i in range(4)]
+        chain = lambda v: torch.cat([F.silu(v), v + v], dim=1)  # noqa: E731
+        graphs = [CapturedForward(chain, x) for x in xs]
+        eager = [chain(x).cpu() for x in xs]
+        for _ in range(3):
+            for g in graphs:
+                g.replay()
+        outs = [g.outputs.clone() for g in graphs]  # eager copies queued behind the replays
+        for got, want in zip(outs, eager):
+            assert bits_equal(got.cpu(), want)
+        # an eager op consuming a replay's output without any synchronize
+        for k in range(5):
+            y = graphs[k % 4].replay()
+            z = torch.mul(y, 0.5)
+            assert bits_equal(z.cpu(), ew.binary_scalar(1, eager[k % 4], 0.5))  # op 1: mul
+        # new inputs between queued replays
+        for k in range(3):
+            v = normal16((2, 8, 20, 20, 16), 950 + k).to(npu)
+            out = graphs[1](v)
+            assert bits_equal(out.cpu(), chain(v).cpu())
+        for g in graphs:
+            g.close()
 
 
 def test_runtime_graph_phases(npu):

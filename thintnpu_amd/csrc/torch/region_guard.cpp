@@ -1,248 +1,285 @@
 // _region_guard: frozen-state guard for captured inference regions.
 //
-// A Guard snapshots, for every nn.Module of a region, what a captured graph
-// silently depends on, and validate() re-checks it before each capture or
-// replay.  The snapshot covers:
-//   - the module's class and its __dict__ object;
-//   - training == False and empty hook dicts;
-//   - the child modules (by identity) and the forward binding (unless the
-//     module is in `ignored`, whose forward the caller swaps itself);
-//   - selected operator attributes (by identity or ==);
-//   - every parameter and buffer: identity, version counter, data pointer,
-//     sizes, strides, offset, dtype, device and requires_grad == False;
-//   - each class's forward, and torch's global module hooks (none allowed).
-// Any drift raises ValueError.  require_frozen_fp16() is the admission rule
-// RegionContract applies before building a Guard.  Python API and messages follow the
-// reference's region guard (region_guard.cpp:36-188, used through
-// region_contract.py:5-28); the implementation is independent.
+// Python surface (the drop-in for the reference's region guard,
+// region_guard.cpp:36-188, used through region_contract.py:5-28):
+//   Guard(modules, ignored, attributes) and Guard.validate(), which raises
+//   ValueError with the message of the first drift it finds;
+//   require_frozen_fp16(modules), the admission rule RegionContract applies
+//   before it builds a Guard.
+//
+// Design.  Building a Guard compiles the region into a check program: a flat
+// list of Checks, each one comparison of a live object against what the
+// snapshot saw, tagged with the ValueError message it raises.  validate()
+// runs the program front to back and stops at the first failing check, so
+// the list order is the order in which drifts are reported:
+//   1. torch's global module hooks are empty;
+//   2. every class's forward is the snapshot's function;
+//   3. per module, in region order: its class, its __dict__ object, training
+//      is False, the four hook dicts are empty, the children (count, then
+//      identity), the forward binding (unless ignored), the operator
+//      attributes, then _parameters and _buffers (count, then per slot the
+//      object's identity and its tensor fingerprint).
+// Reading a key that has disappeared from a module __dict__ raises
+// "Region attribute removed".
 #include <pybind11/pybind11.h>
 #include <torch/csrc/autograd/python_variable.h>
 
 #include <string>
-#include <utility>
 #include <vector>
 
 namespace py = pybind11;
 
 namespace {
 
-// Borrowed lookup in a dict; nullptr when absent (Python errors propagate).
-PyObject* lookup(PyObject* dict, PyObject* key) {
-  PyObject* v = PyDict_GetItemWithError(dict, key);
-  if (!v && PyErr_Occurred()) throw py::error_already_set();
+[[noreturn]] void python_error() { throw py::error_already_set(); }
+
+// d[key] or nullptr (borrowed); lookup errors propagate.
+PyObject* item(PyObject* d, PyObject* key) {
+  PyObject* v = PyDict_GetItemWithError(d, key);
+  if (!v && PyErr_Occurred()) python_error();
   return v;
 }
 
-PyObject* as_dict(PyObject* v) {
+PyObject* require_dict(PyObject* v) {
   if (!v || !PyDict_Check(v)) throw py::value_error("Expected a module state dictionary");
   return v;
 }
 
-Py_ssize_t size_of(PyObject* v) {
+Py_ssize_t length(PyObject* v) {
   const Py_ssize_t n = PyObject_Length(v);
-  if (n < 0) throw py::error_already_set();
+  if (n < 0) python_error();
   return n;
 }
 
-py::str interned(const char* s) {
+py::str name(const char* s) {
   PyObject* v = PyUnicode_InternFromString(s);
-  if (!v) throw py::error_already_set();
+  if (!v) python_error();
   return py::reinterpret_steal<py::str>(v);
 }
 
-// Everything about a parameter/buffer tensor that a captured graph bakes in.
-struct TensorState {
-  bool defined = false;
+// What a captured graph bakes in about a parameter or buffer.
+struct Fingerprint {
   uint32_t version = 0;
   const void* data = nullptr;
-  std::vector<int64_t> sizes, strides;
   int64_t offset = 0;
   c10::ScalarType dtype = c10::ScalarType::Undefined;
   c10::Device device{c10::DeviceType::CPU};
+  std::vector<int64_t> shape;  // sizes followed by strides
+  bool grad = false;
 
-  static TensorState of(const at::Tensor& t) {
-    TensorState s;
-    if (!t.defined()) return s;
-    s.defined = true;
-    s.version = t.unsafeGetTensorImpl()->version_counter().current_version();
-    s.data = t.const_data_ptr();
-    s.sizes = t.sizes().vec();
-    s.strides = t.strides().vec();
-    s.offset = t.storage_offset();
-    s.dtype = t.scalar_type();
-    s.device = t.device();
-    return s;
+  static Fingerprint of(PyObject* tensor) {
+    const at::Tensor& t = THPVariable_Unpack(tensor);
+    Fingerprint f;
+    f.version = t.unsafeGetTensorImpl()->version_counter().current_version();
+    f.data = t.const_data_ptr();
+    f.offset = t.storage_offset();
+    f.dtype = t.scalar_type();
+    f.device = t.device();
+    f.shape = t.sizes().vec();
+    for (int64_t s : t.strides()) f.shape.push_back(s);
+    f.grad = t.requires_grad();
+    return f;
   }
-  bool still(const at::Tensor& t) const {
-    return !t.requires_grad() && t.unsafeGetTensorImpl()->version_counter().current_version() == version &&
-           t.const_data_ptr() == data && t.scalar_type() == dtype && t.device() == device &&
-           t.storage_offset() == offset && t.sizes() == at::IntArrayRef(sizes) &&
-           t.strides() == at::IntArrayRef(strides);
+  bool operator==(const Fingerprint& o) const {
+    return version == o.version && data == o.data && offset == o.offset && dtype == o.dtype &&
+           device == o.device && shape == o.shape && grad == o.grad;
   }
 };
 
-struct Slot {          // one entry of _parameters or _buffers
-  py::str name;
-  py::object value;    // the Tensor object (or None)
-  TensorState state;
+enum class Test {
+  kEmptyAttr,     // len(getattr(subject, key)) == 0
+  kAttrIs,        // getattr(subject, key) is expected
+  kTypeIs,        // type(subject) is expected
+  kDictIs,        // subject.__dict__ is expected
+  kKeyIs,         // subject[key] is expected               (subject: a module __dict__)
+  kKeyEmpty,      // len(subject[key]) == 0
+  kKeyCount,      // len(subject[key]) == count, subject[key] a dict
+  kEntryIs,       // subject[key].get(entry) is expected
+  kForward,       // subject's instance forward, if any, binds expected (function) to bound (self)
+  kKeyEquals,     // subject[key] is, or == , expected; a missing key fails the check
+  kFingerprint,   // the tensor object `expected` still has fingerprint `print`
 };
 
-struct Collection {    // _parameters or _buffers
-  py::str key;
+struct Check {
+  Test test;
+  const char* message;  // the ValueError raised when the check fails
+  py::object subject, key, entry, expected, bound;
   Py_ssize_t count = 0;
-  std::vector<Slot> slots;
+  bool instance_forward = false;
+  Fingerprint print;
 };
 
-struct ModuleState {
-  py::object module, cls, dict;
-  bool guard_forward = true;
-  bool instance_forward = false;      // forward stored in the instance dict
-  py::object forward_func, forward_self;
-  std::vector<std::pair<py::str, py::object>> children, attributes;
-  std::vector<Collection> collections;
-};
+// subject[key], which the snapshot saw: its disappearance is itself a drift.
+PyObject* present(const py::object& subject, const py::object& key) {
+  PyObject* v = item(subject.ptr(), key.ptr());
+  if (!v) throw py::value_error("Region attribute removed");
+  return v;
+}
+
+bool passes(const Check& c) {
+  switch (c.test) {
+    case Test::kEmptyAttr: {
+      py::object v = py::reinterpret_steal<py::object>(PyObject_GetAttr(c.subject.ptr(), c.key.ptr()));
+      if (!v) python_error();
+      return length(v.ptr()) == 0;
+    }
+    case Test::kAttrIs: {
+      py::object v = py::reinterpret_steal<py::object>(PyObject_GetAttr(c.subject.ptr(), c.key.ptr()));
+      if (!v) python_error();
+      return v.ptr() == c.expected.ptr();
+    }
+    case Test::kTypeIs:
+      return reinterpret_cast<PyObject*>(Py_TYPE(c.subject.ptr())) == c.expected.ptr();
+    case Test::kDictIs: {
+      py::object v = py::reinterpret_steal<py::object>(PyObject_GenericGetDict(c.subject.ptr(), nullptr));
+      if (!v) python_error();
+      return v.ptr() == c.expected.ptr();
+    }
+    case Test::kKeyIs:
+      return present(c.subject, c.key) == c.expected.ptr();
+    case Test::kKeyEmpty:
+      return length(present(c.subject, c.key)) == 0;
+    case Test::kKeyCount:
+      return length(require_dict(present(c.subject, c.key))) == c.count;
+    case Test::kEntryIs:
+      return item(require_dict(present(c.subject, c.key)), c.entry.ptr()) == c.expected.ptr();
+    case Test::kForward: {
+      PyObject* f = item(c.subject.ptr(), c.key.ptr());
+      if (!f) return !c.instance_forward;  // the class forward serves, as at the snapshot
+      return PyMethod_Check(f) && PyMethod_Function(f) == c.expected.ptr() && PyMethod_Self(f) == c.bound.ptr();
+    }
+    case Test::kKeyEquals: {
+      PyObject* v = item(c.subject.ptr(), c.key.ptr());
+      if (!v) return false;
+      if (v == c.expected.ptr()) return true;
+      const int eq = PyObject_RichCompareBool(v, c.expected.ptr(), Py_EQ);
+      if (eq < 0) python_error();
+      return eq == 1;
+    }
+    case Test::kFingerprint:
+      return Fingerprint::of(c.expected.ptr()) == c.print;
+  }
+  return false;
+}
 
 class Guard {
  public:
-  Guard(py::iterable modules, py::set ignored, py::iterable attributes)
-      : registry_(py::module_::import("torch.nn.modules.module")) {
-    std::vector<py::str> attrs;
-    for (auto a : attributes) attrs.push_back(py::reinterpret_borrow<py::str>(a));
-    for (auto item : modules) snapshot(py::reinterpret_borrow<py::object>(item), ignored, attrs);
+  Guard(py::iterable modules, py::set ignored, py::iterable attributes) {
+    std::vector<py::object> attrs;
+    for (auto a : attributes) attrs.push_back(py::reinterpret_borrow<py::object>(a));
+
+    py::object registry = py::module_::import("torch.nn.modules.module");
+    for (const char* hooks : {"_global_forward_hooks", "_global_forward_pre_hooks", "_global_backward_hooks",
+                              "_global_backward_pre_hooks"})
+      add(head_, Test::kEmptyAttr, "Global module hooks are unsupported", registry, name(hooks));
+
+    std::vector<Check> body;
+    std::vector<PyObject*> classes;
+    for (auto m : modules) {
+      py::object module = py::reinterpret_borrow<py::object>(m);
+      py::object cls = py::reinterpret_borrow<py::object>(reinterpret_cast<PyObject*>(Py_TYPE(module.ptr())));
+      bool known = false;
+      for (PyObject* c : classes) known = known || c == cls.ptr();
+      if (!known) {
+        classes.push_back(cls.ptr());
+        add(head_, Test::kAttrIs, "Module class forward changed", cls, forward_, py::object(), cls.attr("forward"));
+      }
+      compile_module(body, module, cls, ignored.contains(module), attrs);
+    }
+    head_.insert(head_.end(), std::make_move_iterator(body.begin()), std::make_move_iterator(body.end()));
     validate();
   }
 
   void validate() const {
-    for (const auto& name : global_hooks_) {
-      py::object hooks = py::reinterpret_steal<py::object>(PyObject_GetAttr(registry_.ptr(), name.ptr()));
-      if (!hooks) throw py::error_already_set();
-      if (size_of(hooks.ptr())) throw py::value_error("Global module hooks are unsupported");
-    }
-    for (const auto& [cls, forward] : class_forwards_) {
-      py::object now = py::reinterpret_steal<py::object>(PyObject_GetAttr(cls.ptr(), forward_.ptr()));
-      if (!now) throw py::error_already_set();
-      if (now.ptr() != forward.ptr()) throw py::value_error("Module class forward changed");
-    }
-    for (const auto& m : modules_) check(m);
+    for (const Check& c : head_)
+      if (!passes(c)) throw py::value_error(c.message);
   }
 
  private:
-  void snapshot(py::object module, const py::set& ignored, const std::vector<py::str>& attrs) {
-    ModuleState m;
-    m.module = module;
-    m.cls = py::type::of(module);
-    m.dict = module.attr("__dict__");
-    PyObject* d = as_dict(m.dict.ptr());
-    m.guard_forward = !ignored.contains(module);
-    m.instance_forward = lookup(d, forward_.ptr()) != nullptr;
+  static Check& add(std::vector<Check>& program, Test test, const char* message, py::object subject,
+                    py::object key = py::object(), py::object entry = py::object(),
+                    py::object expected = py::object()) {
+    Check c;
+    c.test = test;
+    c.message = message;
+    c.subject = std::move(subject);
+    c.key = std::move(key);
+    c.entry = std::move(entry);
+    c.expected = std::move(expected);
+    program.push_back(std::move(c));
+    return program.back();
+  }
+
+  void compile_module(std::vector<Check>& out, const py::object& module, const py::object& cls, bool ignored,
+                      const std::vector<py::object>& attrs) {
+    py::object state = module.attr("__dict__");
+    PyObject* d = require_dict(state.ptr());
     py::object bound = module.attr("forward");
     if (!PyMethod_Check(bound.ptr())) throw py::value_error("Expected a bound module forward");
-    m.forward_func = py::reinterpret_borrow<py::object>(PyMethod_Function(bound.ptr()));
-    m.forward_self = py::reinterpret_borrow<py::object>(PyMethod_Self(bound.ptr()));
-    PyObject* children = as_dict(required(d, modules_key_));
+
+    add(out, Test::kTypeIs, "Region module class changed", module, {}, {}, cls);
+    add(out, Test::kDictIs, "Region module dictionary changed", module, {}, {}, state);
+    add(out, Test::kKeyIs, "Region is inference-only", state, training_, {},
+        py::reinterpret_borrow<py::object>(Py_False));
+    for (const char* hooks : {"_forward_hooks", "_forward_pre_hooks", "_backward_hooks", "_backward_pre_hooks"})
+      add(out, Test::kKeyEmpty, "Region hooks changed", state, name(hooks));
+
+    PyObject* children = require_dict(present(state, modules_));
+    add(out, Test::kKeyCount, "Region children changed", state, modules_).count = PyDict_Size(children);
     for (auto kv : py::reinterpret_borrow<py::dict>(children))
-      m.children.emplace_back(py::reinterpret_borrow<py::str>(kv.first), py::reinterpret_borrow<py::object>(kv.second));
-    for (const auto& a : attrs)
-      if (PyObject* v = lookup(d, a.ptr())) m.attributes.emplace_back(a, py::reinterpret_borrow<py::object>(v));
-    for (const auto& key : {params_key_, buffers_key_}) {
-      Collection c;
-      c.key = key;
-      PyObject* values = as_dict(required(d, key));
-      c.count = size_of(values);
-      for (auto kv : py::reinterpret_borrow<py::dict>(values)) {
+      add(out, Test::kEntryIs, "Region child identity changed", state, modules_,
+          py::reinterpret_borrow<py::object>(kv.first), py::reinterpret_borrow<py::object>(kv.second));
+
+    if (!ignored) {
+      Check& f = add(out, Test::kForward, "Region forward changed", state, forward_, {},
+                     py::reinterpret_borrow<py::object>(PyMethod_Function(bound.ptr())));
+      f.bound = py::reinterpret_borrow<py::object>(PyMethod_Self(bound.ptr()));
+      f.instance_forward = item(d, forward_.ptr()) != nullptr;
+    }
+
+    for (const py::object& a : attrs)
+      if (PyObject* v = item(d, a.ptr()))
+        add(out, Test::kKeyEquals, "Region operator configuration changed", state, a, {},
+            py::reinterpret_borrow<py::object>(v));
+
+    for (const py::str* key : {&parameters_, &buffers_}) {
+      PyObject* slots = require_dict(present(state, *key));
+      add(out, Test::kKeyCount, "Region parameter/buffer set changed", state, *key).count = PyDict_Size(slots);
+      for (auto kv : py::reinterpret_borrow<py::dict>(slots)) {
         py::object value = py::reinterpret_borrow<py::object>(kv.second);
         if (!value.is_none() && !THPVariable_Check(value.ptr()))
           throw py::type_error("Expected a Tensor or None in module parameters/buffers");
-        Slot s{py::reinterpret_borrow<py::str>(kv.first), value,
-               value.is_none() ? TensorState{} : TensorState::of(THPVariable_Unpack(value.ptr()))};
-        c.slots.push_back(std::move(s));
-      }
-      m.collections.push_back(std::move(c));
-    }
-    bool seen = false;
-    for (const auto& cf : class_forwards_) seen = seen || cf.first.ptr() == m.cls.ptr();
-    if (!seen) class_forwards_.emplace_back(m.cls, m.cls.attr("forward"));
-    modules_.push_back(std::move(m));
-  }
-
-  static PyObject* required(PyObject* dict, const py::str& key) {
-    PyObject* v = lookup(dict, key.ptr());
-    if (!v) throw py::value_error("Region attribute removed");
-    return v;
-  }
-
-  void check(const ModuleState& m) const {
-    if (reinterpret_cast<PyObject*>(Py_TYPE(m.module.ptr())) != m.cls.ptr())
-      throw py::value_error("Region module class changed");
-    {
-      py::object now = py::reinterpret_steal<py::object>(PyObject_GenericGetDict(m.module.ptr(), nullptr));
-      if (!now) throw py::error_already_set();
-      if (now.ptr() != m.dict.ptr()) throw py::value_error("Region module dictionary changed");
-    }
-    PyObject* d = m.dict.ptr();
-    if (required(d, training_) != Py_False) throw py::value_error("Region is inference-only");
-    for (const auto& h : hook_keys_)
-      if (size_of(required(d, h))) throw py::value_error("Region hooks changed");
-    PyObject* children = as_dict(required(d, modules_key_));
-    if (PyDict_Size(children) != (Py_ssize_t)m.children.size()) throw py::value_error("Region children changed");
-    for (const auto& [name, child] : m.children)
-      if (lookup(children, name.ptr()) != child.ptr()) throw py::value_error("Region child identity changed");
-    if (m.guard_forward) {
-      PyObject* f = lookup(d, forward_.ptr());
-      if (f) {
-        if (!PyMethod_Check(f) || PyMethod_Function(f) != m.forward_func.ptr() ||
-            PyMethod_Self(f) != m.forward_self.ptr())
-          throw py::value_error("Region forward changed");
-      } else if (m.instance_forward) {
-        throw py::value_error("Region forward changed");
-      }
-    }
-    for (const auto& [name, value] : m.attributes) {
-      PyObject* v = lookup(d, name.ptr());
-      if (!v) throw py::value_error("Region operator configuration changed");
-      if (v != value.ptr()) {
-        const int eq = PyObject_RichCompareBool(v, value.ptr(), Py_EQ);
-        if (eq < 0) throw py::error_already_set();
-        if (eq != 1) throw py::value_error("Region operator configuration changed");
-      }
-    }
-    for (const auto& c : m.collections) {
-      PyObject* values = as_dict(required(d, c.key));
-      if (size_of(values) != c.count) throw py::value_error("Region parameter/buffer set changed");
-      for (const auto& s : c.slots) {
-        if (lookup(values, s.name.ptr()) != s.value.ptr())
-          throw py::value_error("Region parameter/prepack identity changed");
-        if (!s.value.is_none() && !s.state.still(THPVariable_Unpack(s.value.ptr())))
-          throw py::value_error("Region parameter/prepack version or gradient mode changed");
+        add(out, Test::kEntryIs, "Region parameter/prepack identity changed", state, *key,
+            py::reinterpret_borrow<py::object>(kv.first), value);
+        if (value.is_none()) continue;
+        Check& t = add(out, Test::kFingerprint, "Region parameter/prepack version or gradient mode changed", state,
+                       {}, {}, value);
+        t.print = Fingerprint::of(value.ptr());
+        t.print.grad = false;  // a frozen region holds no tensor that requires grad
       }
     }
   }
 
-  py::object registry_;
-  std::vector<ModuleState> modules_;
-  std::vector<std::pair<py::object, py::object>> class_forwards_;
-  py::str training_ = interned("training"), modules_key_ = interned("_modules"), forward_ = interned("forward");
-  py::str params_key_ = interned("_parameters"), buffers_key_ = interned("_buffers");
-  std::vector<py::str> hook_keys_{interned("_forward_hooks"), interned("_forward_pre_hooks"),
-                                  interned("_backward_hooks"), interned("_backward_pre_hooks")};
-  std::vector<py::str> global_hooks_{interned("_global_forward_hooks"), interned("_global_forward_pre_hooks"),
-                                     interned("_global_backward_hooks"), interned("_global_backward_pre_hooks")};
+  py::str training_ = name("training"), modules_ = name("_modules"), forward_ = name("forward");
+  py::str parameters_ = name("_parameters"), buffers_ = name("_buffers");
+  std::vector<Check> head_;  // the check program, in reporting order
 };
 
-// Admission rule of a frozen fp16 region (RegionContract's constructor): every
-// parameter and buffer of every module is a version-counted fp16 tensor on the
-// npu device without gradient.  Tensors are visited module by module,
-// parameters before buffers, and the first offender raises ValueError.  An
-// inference-mode tensor has no version counter for the guard to snapshot.
+// Admission rule of a frozen fp16 region (RegionContract's constructor,
+// region_contract.py:15-24 in the reference): every parameter and buffer of
+// every module is a version-counted fp16 tensor on the npu device without
+// gradient.  Tensors are visited module by module, parameters before buffers,
+// and the first offender raises ValueError.  An inference-mode tensor has no
+// version counter for the guard to fingerprint.
 void require_frozen_fp16(py::iterable modules) {
-  const py::str keys[2] = {interned("_parameters"), interned("_buffers")};
-  for (auto item : modules) {
-    py::object state = py::reinterpret_borrow<py::object>(item).attr("__dict__");
-    PyObject* d = as_dict(state.ptr());
+  const py::str keys[2] = {name("_parameters"), name("_buffers")};
+  for (auto m : modules) {
+    py::object state = py::reinterpret_borrow<py::object>(m).attr("__dict__");
+    PyObject* d = require_dict(state.ptr());
     for (const auto& key : keys) {
-      PyObject* values = lookup(d, key.ptr());
-      if (!values) continue;
-      for (auto kv : py::reinterpret_borrow<py::dict>(as_dict(values))) {
+      PyObject* slots = item(d, key.ptr());
+      if (!slots) continue;
+      for (auto kv : py::reinterpret_borrow<py::dict>(require_dict(slots))) {
         if (kv.second.is_none()) continue;
         if (!THPVariable_Check(kv.second.ptr()))
           throw py::type_error("Expected a Tensor or None in module parameters/buffers");

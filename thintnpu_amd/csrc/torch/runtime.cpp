@@ -151,8 +151,13 @@ size_t round_size(size_t n) {
 // was allocated on and is reused only by later allocations on that stream, so
 // reuse is ordered after every kernel that stream enqueued with it.  Work of
 // other streams on the block has finished by the time it is released: eager
-// ops complete before they return (after_launch), and with THIN_ASYNC=1 there
-// is only one stream.
+// ops complete before they return (after_launch; staging and resize copies
+// included), and with THIN_ASYNC=1 there is only one stream.  Graph replays
+// are the exception: they only enqueue.  A block a replay touches is either
+// graph-owned (held until close(), which synchronizes) or state the caller
+// keeps alive while the graph lives (parameters, the captured input); when
+// the graph's own thread frees such a block, it returns to the graph's
+// stream, whose later work is ordered after the replay.
 class Pool {
  public:
   void* alloc(size_t n) {
@@ -338,6 +343,7 @@ const at::Tensor& resize_(const at::Tensor& self, c10::SymIntArrayRef size,
     if (old && impl->storage().data())
       hip_check(hipMemcpyAsync(fresh.mutable_data(), impl->storage().data(), old, hipMemcpyDeviceToDevice, stream()),
                 "hipMemcpyAsync");
+    if (old) after_launch();  // the old storage may be released to another thread
     impl->set_storage_keep_dtype(std::move(fresh));
   }
   impl->set_sizes_contiguous(sizes);
@@ -397,6 +403,7 @@ at::Tensor& copy_(at::Tensor& dst, const at::Tensor& src_in, bool non_blocking) 
     if (!direct) {
       thin_desc s = desc(stage), d = desc(dst);
       check(thin_copy(&s, &d, stream()), "thin copy_");
+      after_launch();  // dst may belong to another thread's stream
     }
     return dst;
   }
@@ -503,8 +510,10 @@ class RuntimeGraph : public torch::CustomClassHolder {
     TORCH_CHECK(phase_ == Phase::kExecutable && exec_.exec, "RuntimeGraph.replay: ", describe(),
                 ", nothing to replay");
     TORCH_CHECK(!capturing(), "RuntimeGraph.replay: cannot launch a graph while this thread records one");
+    // Enqueue only, as the reference's replay does (backend.cpp:89-93).  The
+    // graph's memory stays reserved until close(), which synchronizes; a D2H
+    // copy or synchronize() on this thread waits for the replay.
     hip_check(hipGraphLaunch(exec_.exec, stream_), "hipGraphLaunch");
-    after_launch();
   }
 
   void close() {
