@@ -260,7 +260,46 @@ def test_replays_enqueue_and_stay_ordered(npu):
             v = normal16((2, 8, 20, 20, 16), 950 + k).to(npu)
             out = graphs[1](v)
             assert bits_equal(out.cpu(), chain(v).cpu())
+        assert all(g.graph.direct() for g in graphs)  # three kernels: dispatched directly
         for g in graphs:
+            g.close()
+
+
+def test_replay_dispatch_forms(npu):
+    """Short kernel chains replay by direct dispatch of the recorded kernels,
+    longer ones and recordings holding a copy node through hipGraphLaunch;
+    every form equals the eager result on every replay, with eager work
+    between the replays."""
+    from thin_backend.graph import CapturedForward
+    with torch.inference_mode():
+        x = normal16((1, 4, 16, 16, 16), 960).to(npu)
+        host = normal16((1, 4, 16, 16, 16), 961)
+
+        def one(v):
+            return torch.sigmoid(v)
+
+        def four(v):
+            return torch.cat([F.silu(v), (v + v) * 0.5], dim=1)
+
+        def long(v):
+            y = v
+            for _ in range(6):
+                y = F.silu(y) + v
+            return y
+
+        def with_upload(v):
+            c = host.to(npu)  # a host-to-device copy node in the recording
+            return F.silu(v) + c
+
+        for fn, direct in ((one, True), (four, True), (long, False), (with_upload, False)):
+            g = CapturedForward(fn, x)
+            assert g.graph.direct() == direct, fn.__name__
+            want = fn(x).cpu()
+            for k in range(4):
+                assert bits_equal(g.replay().cpu(), want), (fn.__name__, k)
+                torch.sigmoid(x)  # eager work between replays
+            other = normal16((1, 4, 16, 16, 16), 962 + k).to(npu)
+            assert bits_equal(g(other).cpu(), fn(other).cpu()), fn.__name__
             g.close()
 
 
