@@ -7,7 +7,7 @@ over NC1HWC0 fp16 tensors at the three YOLOv8s neck shapes (C,H,W) in
 and on the C2f half-split narrowed view x[:, C/2:] -- six launches of the
 fused kernel.  ``value`` = algorithmic bytes (each input read once, each output
 written once, 2 B per fp16) of a step / step time, in GB/s, with inputs resident
-in HBM and buffer sets rotated (> 512 MB) so the 256 MB Infinity Cache cannot
+in HBM and buffer sets rotated (>= 1.25 GB) so the 256 MB Infinity Cache cannot
 serve them.  Consecutive steps are replayed from HIP graphs holding 8 steps each
 (every step on its own rotated set); exactly --steps steps are timed.
 
@@ -38,7 +38,9 @@ import torch  # noqa: E402
 
 METRIC = "HBM GB/s (% of peak) + µs/op, YOLOv8s fp16 eltwise/softmax, N=1 & N=32"
 HBM_PEAK_GBS = 8000.0
-ROTATE_BYTES = 640 << 20  # > 2x the 256 MB Infinity Cache
+ROTATE_BYTES = 1280 << 20  # distinct buffer bytes a rotated row cycles through: 5x the 256 MB Infinity Cache
+# (with 2.8x, three sets of the C3 upsample->cat at N=32, rows still came
+# partly from the cache: 35.7 against 49.4 us with six sets)
 GRAPH_STEPS = 8           # bench steps recorded in one HIP graph
 C2_SHAPES = [(128, 80, 80), (256, 40, 40), (512, 20, 20)]
 
@@ -540,6 +542,102 @@ def op_rows(capi, dev):
     return rows
 
 
+# ------------------------------------------------------------------ HBM size sweep
+
+SWEEP_MB = (13, 26, 52, 105, 210, 315)
+FLUSH_BYTES = 512 << 20
+
+
+def sweep_mixes(capi, dev):
+    """(name, read:write mix, factory(target algorithmic bytes) -> (launch,
+    sets, algorithmic bytes)) for the HBM size sweep: plain streaming
+    kernels of the library at several read:write mixes, plus the kernels
+    judged against them (the dominant affine+SiLU, upsample->cat, DFL)."""
+    h = torch.float16
+
+    def dense(m, i):
+        return torch.randn(m, generator=torch.Generator(device=dev).manual_seed(900 + i), device=dev).half()
+
+    def copy(target):
+        m = max(8, int(target) // 4 // 8 * 8)
+        sets = rotated(lambda i: (dense(m, i), torch.empty(m, dtype=h, device=dev)), 4 * m, True)
+        return (lambda st: capi.copy(st[0], st[1])), sets, 4 * m
+
+    def add(target):
+        m = max(8, int(target) // 6 // 8 * 8)
+        sets = rotated(lambda i: (dense(m, i), dense(m, 50 + i), torch.empty(m, dtype=h, device=dev)), 6 * m, True)
+        return (lambda st: capi.binary(capi.ADD, st[0], st[1], out=st[2])), sets, 6 * m
+
+    def fill(target):
+        m = max(8, int(target) // 2 // 8 * 8)
+        sets = rotated(lambda i: (torch.empty(m, dtype=h, device=dev),), 2 * m, True)
+        return (lambda st: capi.fill(st[0], 1.0)), sets, 2 * m
+
+    def images(target, per_image):
+        return max(1, round(target / per_image))
+
+    return [
+        ("copy", "1:1", copy),
+        ("add", "2:1", add),
+        ("fill", "0:1", fill),
+        ("affine_silu_128x80x80", "1:1", lambda t: op_affine_silu(capi, dev, images(t, 3276800), 128, 80, 80,
+                                                                   False, True)),
+        ("upsample_cat_256+128", "1:2", lambda t: op_upsample_cat(capi, dev, images(t, 7372800), True)),
+        ("dfl_expect_64x8400", "16:1", lambda t: op_dfl(capi, dev, images(t, 1142400), True)),
+    ]
+
+
+def fit_line(points):
+    """Least-squares t = t0 + bytes / BW over (bytes, seconds) points:
+    (t0 in us, BW in GB/s, largest relative residual)."""
+    n = len(points)
+    mx = sum(b for b, _ in points) / n
+    my = sum(t for _, t in points) / n
+    sxx = sum((b - mx) ** 2 for b, _ in points)
+    slope = sum((b - mx) * (t - my) for b, t in points) / sxx
+    t0 = my - slope * mx
+    worst = max(abs(t0 + slope * b - t) / t for b, t in points)
+    return t0 * 1e6, 1.0 / slope / 1e9, worst
+
+
+def hbm_sweep(capi, dev, iters):
+    """Rotated launches of each mix at SWEEP_MB sizes, the per-mix fit, and
+    cold-cache times (a 512 MB fill before every launch, its own time taken
+    off) for the N=32 kernels the fits judge."""
+    fits = {}
+    for name, mix, factory in sweep_mixes(capi, dev):
+        points = []
+        for mb in SWEEP_MB:
+            launch, sets, algo = factory(mb * 1e6)
+            t = time_launches(launch, sets, iters)
+            points.append((algo, t))
+            print(json.dumps({"sweep": name, "mix": mix, "bytes": algo, "us": round(t * 1e6, 3),
+                              "GB/s": round(algo / t / 1e9, 1)}), flush=True)
+            del sets
+            torch.cuda.empty_cache()
+        t0, bw, worst = fit_line(points)
+        fits[name] = (t0, bw)
+        print(json.dumps({"fit": name, "mix": mix, "t0_us": round(t0, 3), "GB/s": round(bw, 1),
+                          "pct_peak": round(100 * bw / HBM_PEAK_GBS, 1), "max_rel_residual": round(worst, 4)}),
+              flush=True)
+    scratch = torch.empty(FLUSH_BYTES // 2, dtype=torch.float16, device=dev)
+    fill_t = time_launches(lambda st: capi.fill(scratch, 0.0), [None], max(20, iters // 4))
+    for name, factory in (("affine_silu_128x80x80", lambda: op_affine_silu(capi, dev, 32, 128, 80, 80, False, True)),
+                          ("upsample_cat_256+128", lambda: op_upsample_cat(capi, dev, 32, True)),
+                          ("dfl_expect_64x8400", lambda: op_dfl(capi, dev, 32, True))):
+        launch, sets, algo = factory()
+
+        def flushed(st, launch=launch):
+            capi.fill(scratch, 0.0)
+            launch(st)
+        t = time_launches(flushed, sets, max(20, iters // 4)) - fill_t
+        print(json.dumps({"flushed": name, "N": 32, "bytes": algo, "us": round(t * 1e6, 3),
+                          "GB/s": round(algo / t / 1e9, 1), "fill_512MB_us": round(fill_t * 1e6, 3)}), flush=True)
+        del sets
+        torch.cuda.empty_cache()
+    return fits
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def cpu_op(name, n):
@@ -733,7 +831,8 @@ def main():
                          "calibration): 'dominant', 'copy' (a plain 16-byte copy of the same size), "
                          "'copy@<C>x<H>x<W>' (a copy of one N=32 C2 tensor), 'floor' (a one-element fill: "
                          "the per-launch floor), or 'op:<row name>[@N]' for one row of the per-op table "
-                         "(N=32 by default, rotated)")
+                         "(N=32 by default, rotated), or 'sweep' (rotated launches of plain streaming kernels "
+                         "at several read:write mixes and sizes, each fitted as t = t0 + bytes / BW)")
     ap.add_argument("--ops-json", default=None, help="also write the per-op rows to this file")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -747,6 +846,9 @@ def main():
     capi.lib()
     dev = torch.device("cuda:0")
     n = 32
+    if args.profile == "sweep":
+        hbm_sweep(capi, dev, args.iters)
+        return
     if args.profile and args.profile.startswith("op:c2f_chain_captured"):
         nn = int(args.profile.partition("@")[2] or 32)
         t = time_c2f_captured(nn, args.iters)

@@ -196,3 +196,14 @@ def test_bench_headline_is_one_short_json_line():
                 "pct_peak", "roofline", "cpu_baseline", "higher_is_better", "scaling", "vs_baseline", "data"):
         assert key in parsed, key
     assert "ops" not in parsed and parsed["roofline"]["frac"] == 0.725
+
+
+def test_bench_sweep_fit_recovers_a_line():
+    """The size-sweep fit returns the floor and bandwidth of points lying on
+    t = t0 + bytes / BW, and reports how far the worst point sits off it."""
+    import bench
+    pts = [(b, 1.6e-6 + b / 6.2e12) for b in (13e6, 26e6, 52e6, 105e6, 210e6, 315e6)]
+    t0, bw, worst = bench.fit_line(pts)
+    assert abs(t0 - 1.6) < 1e-9 and abs(bw - 6200.0) < 1e-6 and worst < 1e-12
+    pts[0] = (pts[0][0], pts[0][1] * 1.1)
+    assert bench.fit_line(pts)[2] > 0.05

@@ -173,7 +173,7 @@ def test_dfl_expect_views_and_specials(gpu):
     v = x.transpose(1, 2)  # [2,64,8400] with anchor stride 64
     got = capi.dfl_expect(x.to(gpu).transpose(1, 2)).cpu()
     assert_rel(got, rd.dfl_expect(v, torch.float32), 1e-3, "dfl transposed")
-    for width in (17, 18, 64):  # one-anchor and two-anchor thread forms
+    for width in (17, 18, 20, 24, 64):  # one-, two-, four- and eight-anchor thread forms
         y = normal16((2, 64, width), 7 + width, std=3.0)
         y[0, 3, 2] = float("nan")
         y[0, 20, 5] = float("inf")

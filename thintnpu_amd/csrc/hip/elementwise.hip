@@ -508,7 +508,7 @@ __global__ __launch_bounds__(kThreads) void affine_silu_flat_kernel(AffineFlatPl
 struct FlatGeom {
   uint32_t total, span, plane_vecs, x_row, o_row, c1;
   uint32_t grid2, grid1;  // blocks for two / one vector per thread
-  bool nt, gapped;
+  bool nt;
 };
 
 bool nc1hwc0_dense_plane(const thin_desc* d, int64_t h, int64_t w) {
@@ -544,23 +544,22 @@ bool flat_geom(const thin_desc* x, const thin_desc* out, const thin_desc* const*
   g.c1 = (uint32_t)c1;
   g.grid2 = (uint32_t)((total + kThreads * 2 - 1) / (kThreads * 2));
   g.grid1 = (uint32_t)((total + kThreads - 1) / kThreads);
+  // Streaming loads and stores from kStreamingBytes, for dense tensors and
+  // for views with gaps between images (the C2f narrowed x[:, C/2:]) alike.
+  // With the buffers cold (rotated over 1.25 GB) the narrowed views time
+  // 10.65 / 5.63 / 4.03 us at (128,80,80) / (256,40,40) / (512,20,20), N=32,
+  // against 10.82 / 6.13 / 4.38 us with cached loads (a shallower rotation,
+  // which let the cache serve part of them, had favoured cached loads).
   g.nt = total * 16 >= kStreamingBytes;
-  // Views with gaps between images (the C2f narrowed x[:, C/2:]) read faster
-  // through cached loads, dense tensors through streaming loads
-  // ([32,64,80,80] view of [32,128,80,80]: 9.07 against 10.64 us; the full
-  // tensor: 17.9 against 18.9 us).
-  g.gapped = x_row != 0 && x_row != span;
   return true;
 }
 
 // Two vectors per thread, or one when that leaves fewer than 256 blocks (a
 // single small image): then more blocks shorten the launch.  Streaming
-// stores from kStreamingBytes; streaming loads for dense inputs only.
+// loads and stores from kStreamingBytes.
 #define THIN_FLAT_LAUNCH(KERNEL, g, stream, ...)                                                           \
   do {                                                                                                    \
-    if ((g).nt && (g).gapped)                                                                             \
-      hipLaunchKernelGGL((KERNEL<2, false, true, ##__VA_ARGS__>), dim3((g).grid2), dim3(kThreads), 0, stream, p); \
-    else if ((g).nt)                                                                                      \
+    if ((g).nt)                                                                                           \
       hipLaunchKernelGGL((KERNEL<2, true, true, ##__VA_ARGS__>), dim3((g).grid2), dim3(kThreads), 0, stream, p);  \
     else if ((g).grid2 >= 256)                                                                            \
       hipLaunchKernelGGL((KERNEL<2, false, false, ##__VA_ARGS__>), dim3((g).grid2), dim3(kThreads), 0, stream, p); \
@@ -745,7 +744,10 @@ void launch_plan(const MapPlan<NIN>& p, bool vec, bool nt, hipStream_t stream) {
       const uint32_t grid = (p.units + kThreads * kUnroll - 1) / (kThreads * kUnroll);
       // streaming loads for one input, cached for two or more (the narrowed
       // [32,4,80,80,16] half of [32,8,80,80,16]: SiLU in place 11.6 -> 10.4 us
-      // streaming, a + b of two halves 10.6 cached against 11.4 streaming)
+      // streaming; a + b of the two halves inside the captured C2f tail, where
+      // the halves were just written: 52.4 us per chain cached against 54.8
+      // streaming, though from cold buffers streaming is faster, 14.6 against
+      // 15.4 us)
       if (nt && NIN == 1)
         hipLaunchKernelGGL((map_rows_kernel<T, V, NIN, kUnroll, true, true, Op>), dim3(grid), dim3(kThreads), 0,
                            stream, q);
