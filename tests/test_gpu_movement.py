@@ -344,6 +344,23 @@ def test_sppf_chain(gpu, n):
         check_pool(capi.sppf_nc1hwc0(x.to(gpu), 5, 3).cpu(), mv.sppf_blocked(x, 5, 3), f"packed zero={zero}")
 
 
+def test_pool_twenty_square_planes(gpu):
+    """The compile-time 20x20 form (k5, at least 256 planes: SPPF at a
+    640-pixel input): zero maxima with +0/-0 ties in both orders redone by
+    first-maximum selects inside packed-maximum planes, NaN and infinities,
+    for the single pool and the SPPF chain."""
+    from thintnpu_amd import capi
+    x = to_blocked(normal16((16, 256, 20, 20), 74))
+    for n, c1 in ((0, 1), (3, 7), (15, 15)):
+        plane = -x[n, c1].abs()
+        plane[::3, ::2] = -0.0
+        plane[1::4, 1::3] = 0.0
+        x[n, c1] = plane
+    x[5, 9] = pool_specials(x[5, 9:10])[0]
+    check_pool(capi.maxpool_nc1hwc0(x.to(gpu), 5).cpu(), mv.maxpool_blocked(x, 5), "20x20 maxpool k5")
+    check_pool(capi.sppf_nc1hwc0(x.to(gpu), 5, 3).cpu(), mv.sppf_blocked(x, 5, 3), "20x20 sppf k5 x3")
+
+
 @pytest.mark.parametrize("n", [15, 16])
 def test_pool_block_forms(gpu, n):
     """Under 256 (n, c1) planes a block pools one C0 half of a plane (n=15: 240

@@ -690,14 +690,18 @@ bool pool_kernel_ok(int32_t k) { return k >= 1 && k <= 15 && (k & 1); }
 // inside a border of R -inf pixels; each repeat is a horizontal pass into a
 // second buffer and a vertical pass back into the plane's interior, written
 // to its output slot as it goes.  Every repeat composes the same pool (not a
-// wider window), so +0/-0 ties resolve exactly as chained pools do.  Pooled
-// values are values of x, so x holding no +0/-0 mix lets every repeat take
-// the packed IEEE maximum.  With pool_only (one repeat, no copy of x) the same
-// kernel is the plain max pool for planes that fit LDS.
+// wider window), so +0/-0 ties resolve exactly as chained pools do.  Each
+// pass takes the packed IEEE maximum of its window and redoes with
+// first-maximum selects only the vectors whose maximum has a +0/-0 lane: a
+// nonzero maximum has the same bits whichever tied element supplies it (NaN:
+// any NaN), so only zero maxima depend on the selection order.  With
+// pool_only (one repeat, no copy of x) the same kernel is the plain max pool
+// for planes that fit LDS.
 struct SppfPlan {
   const _Float16* x;
   _Float16* y;
-  int64_t xs[3], ys[3];   // element strides of (n, c1, h); pixels are dense (W stride 16)
+  int64_t xs[2], ys[2];   // element strides of (n, c1)
+  uint32_t xh, yh;        // element strides of h (a plane's offsets fit 32 bits); pixels are dense (W stride 16)
   uint32_t c1, h, w, repeats;
   uint32_t pool_only;     // 1: out holds the last pool only (a plain max pool), no copy of x
   FastDiv div_c1, div_row, div_prow;  // row: w * 2 vectors; padded row: (w + k - 1) * 2
@@ -708,100 +712,98 @@ constexpr size_t kSppfLdsBytes = 144 * 1024;
 // x3: 7.8 us at N=32 and 5.2 us at N=1, against 9.4 and 7.6 with 256)
 constexpr uint32_t kSppfThreads = 1024;
 
+// Whether a window maximum has a +0/-0 lane.
+__device__ __forceinline__ bool has_zero(const _Float16 __attribute__((ext_vector_type(8))) m) {
+  typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+  return __builtin_reduce_min(__builtin_bit_cast(u16x8, m) & (uint16_t)0x7fff) == 0;
+}
+
 // VPP: 16-byte vectors per pixel held by a block.  2: the block pools all 16
 // C0 lanes of its plane; 1: one C0 half (lanes 0-7 or 8-15, block parity), so
 // that a small batch launches twice the blocks (channels pool independently).
-template <int K, bool NT, uint32_t BS, uint32_t VPP>
+// HH, WW: the plane's height and width when fixed at compile time (the 20x20
+// planes of a 640-pixel input's SPPF block: the index arithmetic folds to
+// constants), 0 to read them from the plan.
+template <int K, bool NT, uint32_t BS, uint32_t VPP, uint32_t HH = 0, uint32_t WW = 0>
 __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
   constexpr int R = K / 2;
+  const uint32_t ph = HH ? HH : p.h, pw = HH ? WW : p.w;
+  const uint32_t row_vecs = HH ? WW * VPP : p.div_row.d, prow = HH ? (WW + 2 * R) * VPP : p.div_prow.d;
+  auto row_of = [&](uint32_t i) { return HH ? i / (WW * VPP) : p.div_row.div(i); };
+  auto prow_of = [&](uint32_t i) { return HH ? i / ((WW + 2 * R) * VPP) : p.div_prow.div(i); };
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
   typedef PoolVec<_Float16, 8> PV;
   extern __shared__ __attribute__((aligned(16))) char sppf_lds[];
-  __shared__ uint32_t wave_zero_signs[BS / 64];
   const uint32_t plane = VPP == 2 ? blockIdx.x : blockIdx.x >> 1;
   const uint32_t half = VPP == 2 ? 0u : (blockIdx.x & 1u) * 8u;  // C0 lane offset
   const uint32_t n = p.div_c1.div(plane), c = plane - n * p.c1;
-  const uint32_t row_vecs = p.div_row.d, prow = p.div_prow.d;
-  const uint32_t prows = p.h + 2 * R;
-  const uint32_t tile = prows * prow, htile = prows * row_vecs, outs = p.h * row_vecs;
+  const uint32_t prows = ph + 2 * R;
+  const uint32_t tile = prows * prow, htile = prows * row_vecs, outs = ph * row_vecs;
   PV* in = reinterpret_cast<PV*>(sppf_lds);
   PV* hm = in + tile;
-  PV ninf;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ninf.e[j] = (_Float16)(-__builtin_inff());
+  const h8* ih = reinterpret_cast<const h8*>(in);
+  const h8* hh = reinterpret_cast<const h8*>(hm);
+  const h8 ninf = (h8)(_Float16)(-__builtin_inff());
   const _Float16* xp = p.x + n * p.xs[0] + c * p.xs[1] + half;
   auto slot = [&](uint32_t r) { return p.y + n * p.ys[0] + ((r - p.pool_only) * p.c1 + c) * p.ys[1] + half; };
+  // a pixel vector's element offset inside a plane (32-bit)
+  auto pix = [&](uint32_t row_stride, uint32_t y, uint32_t k) {
+    return y * row_stride + (k / VPP) * 16u + (VPP == 2 ? (k & 1u) * 8u : 0u);
+  };
   // stage the padded plane; copy x to output slot 0
-  u16x8 min_pos = (u16x8)(uint16_t)0xffff, min_neg = (u16x8)(uint16_t)0xffff;
   _Float16* y0 = p.pool_only ? nullptr : slot(0);
   for (uint32_t i = threadIdx.x; i < tile; i += BS) {
-    const uint32_t rr = p.div_prow.div(i), k = i - rr * prow;
-    const int xx = (int)(k / VPP) - R, yy = (int)rr - R;
-    PV v = ninf;
-    if (yy >= 0 && yy < (int)p.h && xx >= 0 && xx < (int)p.w) {
-      const int64_t off = (int64_t)yy * p.xs[2] + (int64_t)xx * 16 + (VPP == 2 ? (k & 1u) * 8 : 0u);
-      v = *reinterpret_cast<const PV*>(xp + off);
-      const u16x8 b = __builtin_bit_cast(u16x8, v);
-      min_pos = __builtin_elementwise_min(min_pos, b);
-      min_neg = __builtin_elementwise_min(min_neg, b ^ (uint16_t)0x8000);
+    const uint32_t rr = prow_of(i), k = i - rr * prow;
+    const uint32_t xx = k / VPP - R, yy = rr - R;  // wraps for the -inf border
+    h8 v = ninf;
+    if (yy < ph && xx < pw) {
+      const uint32_t kk = k - R * VPP;
+      v = *reinterpret_cast<const h8*>(xp + pix(p.xh, yy, kk));
       if (!p.pool_only) {
-        const h8 hv = __builtin_bit_cast(h8, v);
-        h8* dst = reinterpret_cast<h8*>(y0 + (int64_t)yy * p.ys[2] + (int64_t)xx * 16 + (VPP == 2 ? (k & 1u) * 8 : 0u));
-        if constexpr (NT) __builtin_nontemporal_store(hv, dst);
-        else *dst = hv;
+        h8* dst = reinterpret_cast<h8*>(y0 + pix(p.yh, yy, kk));
+        if constexpr (NT) __builtin_nontemporal_store(v, dst);
+        else *dst = v;
       }
     }
-    in[i] = v;
-  }
-  {
-    const uint32_t has = (__ballot(__builtin_reduce_min(min_pos) == 0) != 0 ? 1u : 0u) |
-                         (__ballot(__builtin_reduce_min(min_neg) == 0) != 0 ? 2u : 0u);
-    if ((threadIdx.x & 63u) == 0) wave_zero_signs[threadIdx.x >> 6] = has;
+    reinterpret_cast<h8*>(in)[i] = v;
   }
   __syncthreads();
-  uint32_t has = 0;
-#pragma unroll
-  for (int wv = 0; wv < (int)(BS / 64); ++wv) has |= wave_zero_signs[wv];
-  const bool exact = has == 3u;
   for (uint32_t rep = 1; rep <= p.repeats; ++rep) {
     for (uint32_t i = threadIdx.x; i < htile; i += BS) {
-      const uint32_t rr = p.div_row.div(i), k = i - rr * row_vecs;
+      const uint32_t rr = row_of(i), k = i - rr * row_vecs;
       const uint32_t base = rr * prow + k;
-      if (!exact) {
-        const h8* ih = reinterpret_cast<const h8*>(in);
-        h8 m = ih[base];
+      h8 m = ih[base];
 #pragma unroll
-        for (int j = 1; j <= 2 * R; ++j) m = __builtin_elementwise_maximum(m, ih[base + VPP * j]);
-        reinterpret_cast<h8*>(hm)[i] = m;
-      } else {
-        PV m = ninf;
+      for (int j = 1; j <= 2 * R; ++j) m = __builtin_elementwise_maximum(m, ih[base + VPP * j]);
+      if (has_zero(m)) {  // first maximum in window order
+        PV e;
 #pragma unroll
-        for (int j = 0; j <= 2 * R; ++j) keep_max(m, in[base + VPP * j]);
-        hm[i] = m;
+        for (int j = 0; j < 8; ++j) e.e[j] = (_Float16)(-__builtin_inff());
+#pragma unroll
+        for (int j = 0; j <= 2 * R; ++j) keep_max(e, in[base + VPP * j]);
+        m = __builtin_bit_cast(h8, e);
       }
+      reinterpret_cast<h8*>(hm)[i] = m;
     }
     __syncthreads();
     _Float16* yr = slot(rep);
     for (uint32_t i = threadIdx.x; i < outs; i += BS) {
-      const uint32_t r = p.div_row.div(i), k = i - r * row_vecs;
-      PV m;
-      if (!exact) {
-        const h8* hh = reinterpret_cast<const h8*>(hm);
-        h8 mh = hh[r * row_vecs + k];
+      const uint32_t r = row_of(i), k = i - r * row_vecs;
+      h8 m = hh[r * row_vecs + k];
 #pragma unroll
-        for (int dy = 1; dy <= 2 * R; ++dy) mh = __builtin_elementwise_maximum(mh, hh[(r + dy) * row_vecs + k]);
-        m = __builtin_bit_cast(PV, mh);
-      } else {
-        m = ninf;
+      for (int dy = 1; dy <= 2 * R; ++dy) m = __builtin_elementwise_maximum(m, hh[(r + dy) * row_vecs + k]);
+      if (has_zero(m)) {
+        PV e;
 #pragma unroll
-        for (int dy = 0; dy <= 2 * R; ++dy) keep_max(m, hm[(r + dy) * row_vecs + k]);
+        for (int j = 0; j < 8; ++j) e.e[j] = (_Float16)(-__builtin_inff());
+#pragma unroll
+        for (int dy = 0; dy <= 2 * R; ++dy) keep_max(e, hm[(r + dy) * row_vecs + k]);
+        m = __builtin_bit_cast(h8, e);
       }
-      if (rep < p.repeats) in[(r + R) * prow + k + VPP * R] = m;  // the next repeat's input
-      const h8 hv = __builtin_bit_cast(h8, m);
-      h8* dst = reinterpret_cast<h8*>(yr + (int64_t)r * p.ys[2] + (int64_t)(k / VPP) * 16 + (VPP == 2 ? (k & 1u) * 8 : 0u));
-      if constexpr (NT) __builtin_nontemporal_store(hv, dst);
-      else *dst = hv;
+      if (rep < p.repeats) reinterpret_cast<h8*>(in)[(r + R) * prow + k + VPP * R] = m;  // the next repeat's input
+      h8* dst = reinterpret_cast<h8*>(yr + pix(p.yh, r, k));
+      if constexpr (NT) __builtin_nontemporal_store(m, dst);
+      else *dst = m;
     }
     __syncthreads();
   }
@@ -811,6 +813,17 @@ __global__ __launch_bounds__(BS) void sppf_kernel(SppfPlan p) {
 // maxima, vpp 16-byte vectors per pixel.
 uint64_t sppf_lds_bytes(int64_t H, int64_t W, int R, int64_t vpp) {
   return (uint64_t)(H + 2 * R) * (uint64_t)((W + 2 * R) + W) * (uint64_t)vpp * 16u;
+}
+
+// Whether sppf_kernel takes x / out: the padded plane fits one block's LDS,
+// the planes number under 2^31, and every offset inside a plane (rows at
+// strides[2], pixels 16 elements apart) fits 31 bits.
+bool sppf_whole_plane(const thin_desc* x, const thin_desc* out, int R) {
+  const int64_t H = x->sizes[2], W = x->sizes[3];
+  if (sppf_lds_bytes(H, W, R, 2) > kSppfLdsBytes || x->sizes[0] * x->sizes[1] >= ((int64_t)1 << 31)) return false;
+  for (const thin_desc* d : {x, out})
+    if (d->strides[2] < 0 || (H - 1) * d->strides[2] + W * 16 >= ((int64_t)1 << 31)) return false;
+  return true;
 }
 
 // Launches sppf_kernel for x [N,C1,H,W,16] (validated by the caller, whose
@@ -824,10 +837,12 @@ thin_status launch_sppf(const thin_desc* x, int32_t kernel, int32_t repeats, boo
   memset(&p, 0, sizeof p);
   p.x = static_cast<const _Float16*>(x->data);
   p.y = static_cast<_Float16*>(out->data);
-  for (int d = 0; d < 3; ++d) {
+  for (int d = 0; d < 2; ++d) {
     p.xs[d] = x->strides[d];
     p.ys[d] = out->strides[d];
   }
+  p.xh = (uint32_t)x->strides[2];
+  p.yh = (uint32_t)out->strides[2];
   p.c1 = (uint32_t)C1;
   p.h = (uint32_t)H;
   p.w = (uint32_t)W;
@@ -843,6 +858,14 @@ thin_status launch_sppf(const thin_desc* x, int32_t kernel, int32_t repeats, boo
   p.div_prow = FastDiv::make((uint32_t)((W + 2 * R) * vpp));
   const bool nt = numel(out) * 2 >= kStreamingBytes;
   const uint32_t blocks = (uint32_t)(N * C1 * (split ? 2 : 1));
+  if (!split && H == 20 && W == 20 && kernel == 5) {  // SPPF of a 640-pixel input's stride-32 level
+    if (nt) hipLaunchKernelGGL((sppf_kernel<5, true, kSppfThreads, 2, 20, 20>), dim3(blocks), dim3(kSppfThreads),
+                               lds, stream, p);
+    else hipLaunchKernelGGL((sppf_kernel<5, false, kSppfThreads, 2, 20, 20>), dim3(blocks), dim3(kSppfThreads),
+                            lds, stream, p);
+    THIN_LAUNCH_CHECK("sppf");
+    return THIN_OK;
+  }
   switch (kernel) {
 #define THIN_SPPF(KK)                                                                                        \
   case KK:                                                                                                   \
@@ -1243,10 +1266,7 @@ extern "C" thin_status thin_maxpool_nc1hwc0(const thin_desc* x, int32_t kernel, 
   {
     // planes that fit one block's LDS: the whole-plane kernel with one pool
     // (SPPF k5 [32,256,20,20]: 5.2 us, against 7.5 us with row bands)
-    const int R = kernel / 2;
-    if (sppf_lds_bytes(x->sizes[2], x->sizes[3], R, 2) <= kSppfLdsBytes &&
-        x->sizes[0] * x->sizes[1] < ((int64_t)1 << 31))
-      return launch_sppf(x, kernel, 1, true, out, stream);
+    if (sppf_whole_plane(x, out, kernel / 2)) return launch_sppf(x, kernel, 1, true, out, stream);
   }
   PoolPlan p;
   memset(&p, 0, sizeof p);
@@ -1283,8 +1303,7 @@ extern "C" thin_status thin_sppf_nc1hwc0(const thin_desc* x, int32_t kernel, int
                  d->strides[1] % 8 == 0 && d->strides[2] % 8 == 0, THIN_ERR_UNSUPPORTED,
                  "sppf needs 16-byte aligned pixels (C0 dense, W stride 16)");
   THIN_REQUIRE(H < (1 << 30) && W < (1 << 30), THIN_ERR_UNSUPPORTED, "sppf: plane too large");
-  const int R = kernel / 2;
-  if (sppf_lds_bytes(H, W, R, 2) > kSppfLdsBytes || N * C1 >= ((int64_t)1 << 31)) {
+  if (!sppf_whole_plane(x, out, kernel / 2)) {
     // planes beyond one block's LDS: the copy and the chained pools, each
     // reading the previous output slot
     auto slot = [&](int r) {
