@@ -196,6 +196,11 @@ def test_bench_headline_is_one_short_json_line():
                 "pct_peak", "roofline", "cpu_baseline", "higher_is_better", "scaling", "vs_baseline", "data"):
         assert key in parsed, key
     assert "ops" not in parsed and parsed["roofline"]["frac"] == 0.725
+    # over-long free text is shortened, never an error at the end of a run
+    cpu["sample"] = "s" * 10000
+    line = bench.headline(value=4974.1, step_s=55.3e-6, steps=50, warmup=10, batch=32, launches=6,
+                          step_bytes=275256576, nrot=3, roofline=roofline, cpu=cpu, op_rows=120)
+    assert len(json.dumps(line)) <= bench.HEADLINE_MAX_BYTES and line["cpu_baseline"]["value"] == 14.1
 
 
 def test_bench_sweep_fit_recovers_a_line():
