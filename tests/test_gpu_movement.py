@@ -135,6 +135,22 @@ def test_upsample_blocked_bit_patterns(gpu):
     assert bits_equal(capi.upsample2x_nc1hwc0(xt.to(gpu).transpose(2, 3)).cpu(), mv.upsample2x_blocked(vt))
 
 
+def test_upsample_streaming_block_windows(gpu):
+    """Streaming upsample launches (output >= 4 MB) run their blocks in XCD
+    runs of 32 tiles per window of 256 blocks: grids of whole windows only
+    and grids with a partial last window (whose blocks keep their order),
+    alone and with a copied input beside the upsampled one."""
+    from thintnpu_amd import capi
+    for n, c1, h, w in ((3, 16, 40, 40), (1, 64, 28, 36), (5, 7, 33, 31), (2, 12, 51, 49)):
+        x = random_bits16((n, c1, h, w, 16), n * c1 + h)
+        o = random_bits16((n, 3, 2 * h, 2 * w, 16), w)
+        assert n * c1 * 4 * h * w * 32 >= 4 << 20  # the streaming form
+        xd, od = x.to(gpu), o.to(gpu)
+        assert bits_equal(capi.upsample2x_nc1hwc0(xd).cpu(), mv.upsample2x_blocked(x)), (n, c1, h, w)
+        fused = capi.upsample_cat_nc1hwc0([od, xd], [False, True]).cpu()
+        assert bits_equal(fused, mv.upsample_cat_blocked([o, x], [False, True])), (n, c1, h, w)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_upsample_nchw(gpu, dtype):
     """verify_all.py:88-94 shapes, atol 0."""

@@ -118,6 +118,20 @@ namespace dev {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Dispatch deals the workgroups of a launch to the 8 XCDs round robin (block
+// b runs on XCD b % 8, each XCD with its own L2).  xcd_grouped<RUN>(b, nb) is
+// the logical block that b runs as when each XCD is to take runs of RUN
+// consecutive logical blocks (neighbours that read the same lines then share
+// an L2), the 8 runs of each window of 8 * RUN logical blocks side by side
+// (so that the launch still sweeps memory as one front).  Blocks past the
+// last whole window keep their index; the map is a bijection on [0, nb).
+template <uint32_t RUN>
+__device__ __forceinline__ uint32_t xcd_grouped(uint32_t b, uint32_t nb) {
+  constexpr uint32_t kSpan = 8 * RUN;
+  if (b >= nb / kSpan * kSpan) return b;
+  return b / kSpan * kSpan + (b & 7u) * RUN + b % kSpan / 8u;
+}
+
 // NaN-propagating maximum (fmaxf would drop a NaN operand).
 __device__ __forceinline__ float max_nan(float a, float b) {
   return (a > b || a != a) ? a : b;
