@@ -47,8 +47,13 @@ int64_t numel(const thin_desc* d);
 bool same_sizes(const thin_desc* a, const thin_desc* b);
 bool is_contiguous(const thin_desc* d);
 
-// Magic-number unsigned division, exact for n < 2^31 and any 1 <= d < 2^31
-// (round-up multiplier method: q = umulhi(n, mul) >> shr).
+// Magic-number unsigned division, exact for n < 2^31 and any 1 <= d < 2^31,
+// with no branch: q = (umulhi(n, mul) + n) >> shr, shr = ceil(log2 d),
+// mul = floor(2^32 (2^shr - d) / d) + 1 (Granlund and Montgomery's round-up
+// multiplier, its 33rd bit carried by the add of n; n < 2^31 keeps the sum in
+// 32 bits).  d = 1 is mul = 1, shr = 0.  Being branch-free, a kernel reads all
+// three fields in one round of scalar loads (a `d == 1` test put the loads of
+// mul and shr behind a wait).
 struct FastDiv {
   uint32_t d;
   uint32_t mul;
@@ -56,22 +61,21 @@ struct FastDiv {
   static FastDiv make(uint32_t divisor) {
     FastDiv f;
     f.d = divisor;
-    if (divisor <= 1) {
+    if (divisor == 0 || divisor > (1u << 31)) {  // no quotient to give (d = 0), or 0 for every n < 2^31
       f.mul = 0;
-      f.shr = 0;
+      f.shr = 31;
     } else {
-      uint32_t l = 32u - (uint32_t)__builtin_clz(divisor - 1u);  // ceil(log2(d))
-      uint64_t p = 31u + l;
-      f.mul = (uint32_t)(((1ull << p) + divisor - 1u) / divisor);
-      f.shr = (uint32_t)(p - 32u);
+      const uint32_t l = divisor == 1u ? 0u : 32u - (uint32_t)__builtin_clz(divisor - 1u);  // ceil(log2(d))
+      f.mul = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << l) - divisor)) / divisor + 1u);
+      f.shr = l;
     }
     return f;
   }
   __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
 #if defined(__HIP_DEVICE_COMPILE__)
-    return d == 1u ? n : (__umulhi(n, mul) >> shr);
+    return (__umulhi(n, mul) + n) >> shr;
 #else
-    return d == 1u ? n : (uint32_t)((((uint64_t)n * mul) >> 32) >> shr);
+    return (uint32_t)(((((uint64_t)n * mul) >> 32) + n) >> shr);
 #endif
   }
 };
