@@ -122,6 +122,14 @@ namespace dev {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Holds v in a scalar register at this point of the kernel: a kernel
+// argument passed here is loaded before the branches that follow, in the same
+// round of scalar loads as the ones they test, instead of after them.
+template <typename T>
+__device__ __forceinline__ void scalar_here(T v) {
+  __asm__ volatile("" ::"s"(v));
+}
+
 // Dispatch deals the workgroups of a launch to the 8 XCDs round robin (block
 // b runs on XCD b % 8, each XCD with its own L2).  xcd_grouped<RUN>(b, nb) is
 // the logical block that b runs as when each XCD is to take runs of RUN

@@ -297,19 +297,21 @@ template <typename T, int V, int NIN, int U, bool NTL, bool NT, class Op>
 __global__ __launch_bounds__(kThreads) void map_rows_kernel(MapPlan<NIN> p) {
   const uint32_t tile = blockIdx.x * (kThreads * U);
   const FastDiv& rows = p.div[0];  // vectors per row: size[0] / V
+  dev::scalar_here(p.out);
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) dev::scalar_here(p.in[k]);
   VecT<T, V> raw[U][NIN];
   int32_t oo[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t unit = tile + u * kThreads + threadIdx.x;
-    if (unit < p.units) {
-      const uint32_t r = rows.div(unit);
-      const int32_t c = (int32_t)((unit - r * rows.d) * V);  // row strides may be negative
-      oo[u] = (int32_t)r * p.ostride[1] + c;
+    // clamped, not predicated, as in map_dense_kernel
+    const uint32_t unit = min(tile + u * kThreads + threadIdx.x, p.units - 1);
+    const uint32_t r = rows.div(unit);
+    const int32_t c = (int32_t)((unit - r * rows.d) * V);  // row strides may be negative
+    oo[u] = (int32_t)r * p.ostride[1] + c;
 #pragma unroll
-      for (int k = 0; k < NIN; ++k)
-        raw[u][k] = load16<NTL, VecT<T, V>>(static_cast<const T*>(p.in[k]) + ((int32_t)r * p.istride[k][1] + c));
-    }
+    for (int k = 0; k < NIN; ++k)
+      raw[u][k] = load16<NTL, VecT<T, V>>(static_cast<const T*>(p.in[k]) + ((int32_t)r * p.istride[k][1] + c));
   }
   const Op op;
 #pragma unroll
@@ -356,15 +358,20 @@ __global__ __launch_bounds__(kThreads) void map_scalar_kernel(MapPlan<NIN> p) {
 template <typename T, int V, int NIN, int U, bool NT, class Op>
 __global__ __launch_bounds__(kThreads) void map_dense_kernel(MapPlan<NIN> p) {
   const uint32_t tile = blockIdx.x * (kThreads * U);
+  // The operand pointers in registers before any bounds test, and loads
+  // clamped to the last unit instead of predicated: the plan's scalar loads
+  // go out in one round (a test on p.units first made the pointer loads wait
+  // for it).  Stores stay predicated.
+  dev::scalar_here(p.out);
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) dev::scalar_here(p.in[k]);
   VecT<T, V> raw[U][NIN];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t unit = tile + u * kThreads + threadIdx.x;
-    if (unit < p.units) {
+    const uint32_t unit = min(tile + u * kThreads + threadIdx.x, p.units - 1);
 #pragma unroll
-      for (int k = 0; k < NIN; ++k)
-        raw[u][k] = load16<NT, VecT<T, V>>(static_cast<const T*>(p.in[k]) + (size_t)unit * V);
-    }
+    for (int k = 0; k < NIN; ++k)
+      raw[u][k] = load16<NT, VecT<T, V>>(static_cast<const T*>(p.in[k]) + (size_t)unit * V);
   }
   const Op op;
 #pragma unroll
@@ -719,6 +726,7 @@ constexpr int kUnroll = 2;
 template <typename T, int NIN, int ND, class Op>
 void launch_plan(const MapPlan<NIN>& p, bool vec, bool nt, hipStream_t stream) {
   constexpr int V = 16 / (int)sizeof(T);
+  if (p.units == 0) return;  // the dense and row kernels clamp to unit units - 1
   if constexpr (ND == 1) {
     bool dense = vec && p.out_mode == kVec;
     for (int k = 0; k < NIN; ++k) dense = dense && p.in_mode[k] == kVec;

@@ -467,8 +467,9 @@ struct DflPlan {
 template <typename TO, int V, bool FAST, int LOAD>
 __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
   static_assert(V == 1 || V == 2, "one or two anchors per thread");
-  const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
-  if (u >= p.units) return;
+  // threads past the end recompute the last unit and store nothing: no
+  // early exit, so the plan's scalar loads all go out in one round
+  const uint32_t u0 = blockIdx.x * kThreads + threadIdx.x, u = min(u0, p.units - 1);
   const uint32_t side = p.div_avecs.div(u);
   const uint32_t a0 = (u - side * p.avecs) * V;
   const uint32_t n = side >> 2, sd = side & 3u;
@@ -482,6 +483,7 @@ __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
   }
   float r[V];
   dev::dfl_side<V, FAST>(bins, r);
+  if (u0 >= p.units) return;
   TO* op = static_cast<TO*>(p.out);
   if constexpr (LOAD > 0) op += n * (uint32_t)p.on + sd * (uint32_t)p.os + a0 * (uint32_t)p.oa;
   else op += n * p.on + (int64_t)sd * p.os + (int64_t)a0 * p.oa;
