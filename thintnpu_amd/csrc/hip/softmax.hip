@@ -56,11 +56,17 @@ struct SoftmaxPlan {
   int64_t xr, orr;     // reduction strides (column kernel)
 };
 
+// The innermost dim is taken with no test on p.nd (a plan with nd = 0 has
+// zero strides there), so its fields load in the kernel's first round of
+// scalar loads; the rest follow only where nd asks for them.
 __device__ __forceinline__ void col_offsets(const SoftmaxPlan& p, uint32_t e, int64_t& xo, int64_t& oo) {
-  xo = 0;
-  oo = 0;
+  const uint32_t q0 = p.div[0].div(e);
+  const int64_t c0 = (int64_t)(e - q0 * p.size[0]);
+  xo = c0 * p.xs[0];
+  oo = c0 * p.os[0];
+  e = q0;
 #pragma unroll
-  for (int d = 0; d < kMaxDims; ++d) {
+  for (int d = 1; d < kMaxDims; ++d) {
     if (d >= p.nd) break;
     const uint32_t q = p.div[d].div(e);
     const int64_t c = (int64_t)(e - q * p.size[d]);
@@ -91,8 +97,10 @@ __global__ __launch_bounds__(kThreads) void softmax_row_kernel(SoftmaxPlan p) {
   const uint32_t g = lane % G;
   const uint32_t row = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * RPW + lane / G;
   const bool live = row < p.units;  // every lane still joins the group shuffles
-  int64_t xo = 0, oo = 0;
-  if (live) col_offsets(p, row, xo, oo);
+  // offsets of a clamped row rather than under a test of live, so that the
+  // plan's scalar loads are not held behind the load of p.units
+  int64_t xo, oo;
+  col_offsets(p, min(row, p.units - 1), xo, oo);
   const TI* xr = static_cast<const TI*>(p.x) + xo;
   TO* orow = static_cast<TO*>(p.out) + oo;
   const uint32_t chunks = VEC ? p.R / VE : p.R;
