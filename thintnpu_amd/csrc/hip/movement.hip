@@ -238,7 +238,6 @@ struct PlanePlan {
   FastDiv div_row;             // ow * vpp (vectors per output row)
   FastDiv div_vpp;
   FastDiv div_c1;              // out_c1_total
-  uint32_t xcd_runs;           // 1: blocks run as xcd_grouped<kPlaneXcdRun> logical blocks
 };
 constexpr uint32_t kPlaneXcdRun = 32;
 
@@ -249,14 +248,18 @@ constexpr uint32_t kPlaneXcdRun = 32;
 // plane.  (A flat grid over all output vectors chose the input per lane,
 // which put vector loads of the plan in front of every data load: 49.3 against
 // 39.4 us for the C3 upsample->cat at N=32 from cold buffers.)
-template <int U, bool NT, uint32_t BS>
+// NIN: the launch's input count when 1 or 2, else kPlaneInputs (at most that many).
+template <int U, bool NT, uint32_t BS, bool XCD, int NIN>
 __global__ __launch_bounds__(BS) void plane_kernel(PlanePlan p) {
-  // Streaming launches that upsample: consecutive tiles read the same source
-  // rows, so each XCD takes runs of kPlaneXcdRun consecutive tiles.  (Upsample
-  // [32,256,40,40] 25.0 -> 23.9 us, upsample->cat 39.9 -> 39.1 us; runs of
-  // 16 or 64 tiles measured between, one contiguous range per XCD 26.0 and
-  // 42.3 us, small launches slightly slower with any grouping.)
-  const uint32_t blk = p.xcd_runs ? dev::xcd_grouped<kPlaneXcdRun>(blockIdx.x, gridDim.x) : blockIdx.x;
+  // XCD (streaming launches that upsample): consecutive tiles read the same
+  // source rows, so each XCD takes runs of kPlaneXcdRun consecutive tiles.
+  // (Upsample [32,256,40,40] 25.0 -> 23.9 us, upsample->cat 39.9 -> 39.1 us;
+  // runs of 16 or 64 tiles measured between, one contiguous range per XCD
+  // 26.0 and 42.3 us, small launches slightly slower with any grouping.)  A
+  // compile-time choice: a test of a plan field here held every later scalar
+  // load behind its wait (with NIN: upsample 23.1 -> 21.8 us at N=32,
+  // 3.70 -> 3.21 us at N=1).
+  const uint32_t blk = XCD ? dev::xcd_grouped<kPlaneXcdRun>(blockIdx.x, gridDim.x) : blockIdx.x;
   const uint32_t plane = p.div_tiles.div(blk);
   const uint32_t tile = blk - plane * p.tiles;
   const uint32_t n = p.div_c1.div(plane);
@@ -265,8 +268,8 @@ __global__ __launch_bounds__(BS) void plane_kernel(PlanePlan p) {
   // then one round of scalar loads of its record
   uint32_t i = 0;
 #pragma unroll
-  for (int j = 1; j < kPlaneInputs; ++j)
-    if (j < p.count && c1 >= p.c1_prefix[j]) i = j;
+  for (int j = 1; j < NIN; ++j)
+    if ((NIN <= 2 || j < p.count) && c1 >= p.c1_prefix[j]) i = j;
   const PlaneInput& in = p.in[i];
   const char* src = in.src + (int64_t)n * in.src_n + (int64_t)(c1 - in.c1_first) * in.src_c1;
   char* dst = p.out + (int64_t)n * p.out_n + (int64_t)c1 * p.out_c1;
@@ -358,12 +361,24 @@ thin_status launch_planes(const thin_desc* ins, const int32_t* up, int count, co
   THIN_REQUIRE(blocks < (1ull << 31), THIN_ERR_UNSUPPORTED, "upsample/cat: output too large for one launch");
   bool upsamples = false;
   for (int k = 0; k < count; ++k) upsamples = upsamples || p.in[k].up;
-  p.xcd_runs = nt && upsamples ? 1u : 0u;
-  if (nt)
-    hipLaunchKernelGGL((plane_kernel<2, true, kStreamThreads>), dim3((uint32_t)blocks), dim3(kStreamThreads), 0,
-                       stream, p);
-  else
-    hipLaunchKernelGGL((plane_kernel<1, false, kThreads>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
+  // the launch's input count fixed at compile time when it is 1 or 2 (upsample,
+  // upsample->cat): fewer rounds of scalar loads to choose the input
+#define THIN_PLANES(NIN)                                                                                       \
+  do {                                                                                                         \
+    if (nt && upsamples) /* XCD-grouped block order */                                                         \
+      hipLaunchKernelGGL((plane_kernel<2, true, kStreamThreads, true, NIN>), dim3((uint32_t)blocks),           \
+                         dim3(kStreamThreads), 0, stream, p);                                                  \
+    else if (nt)                                                                                               \
+      hipLaunchKernelGGL((plane_kernel<2, true, kStreamThreads, false, NIN>), dim3((uint32_t)blocks),          \
+                         dim3(kStreamThreads), 0, stream, p);                                                  \
+    else                                                                                                       \
+      hipLaunchKernelGGL((plane_kernel<1, false, kThreads, false, NIN>), dim3((uint32_t)blocks), dim3(kThreads), \
+                         0, stream, p);                                                                        \
+  } while (0)
+  if (count == 1) THIN_PLANES(1);
+  else if (count == 2) THIN_PLANES(2);
+  else THIN_PLANES(kPlaneInputs);
+#undef THIN_PLANES
   THIN_LAUNCH_CHECK("plane");
   return THIN_OK;
 }
