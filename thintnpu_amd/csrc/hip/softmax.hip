@@ -553,6 +553,13 @@ constexpr uint32_t kDecodeScoreUnits = VS == 8 ? 2u : 1u;
 // output stores (launches of at least kStreamingBytes).
 template <int VB, int VS, int LOAD>
 __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
+  // The score role's plan fields (most blocks take that role) in registers
+  // before the test of the role: they then load in the same round of scalar
+  // loads as p.box_blocks, not in two more behind it.
+  // (One statement: each inline asm is a scheduling boundary of its own.)
+  __asm__ volatile("" ::"s"(p.scores), "s"(p.out), "s"(p.sb), "s"(p.sc), "s"(p.sa), "s"(p.ob), "s"(p.oc),
+                   "s"(p.oa), "s"(p.score_units), "s"(p.svecs), "s"(p.nc), "s"(p.div_svecs.mul),
+                   "s"(p.div_svecs.shr), "s"(p.div_nc.mul), "s"(p.div_nc.shr), "s"(p.box_blocks));
   if (blockIdx.x < p.box_blocks) {
     const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
     if (u >= p.box_units) return;
