@@ -115,7 +115,7 @@ def time_launches(launch, sets, iters, rounds=5):
 # `bench.py --profile dominant --iters 20` (profiles/affine_silu_flat_n32_128x80x80_pmc.md).
 # Every request is counted once at its size, so bytes = sum(size x count)
 # without any calibration; write requests that are not 64-byte are 32-byte.
-DOMINANT_REQUESTS = {"RDREQ_32B": 0, "RDREQ_64B": 320, "RDREQ_128B": 409632, "WRREQ": 819202, "WRREQ_64B": 819202}
+DOMINANT_REQUESTS = {"RDREQ_32B": 0, "RDREQ_64B": 320, "RDREQ_128B": 409632, "WRREQ": 819200, "WRREQ_64B": 819200}
 
 
 def dominant_traffic():
