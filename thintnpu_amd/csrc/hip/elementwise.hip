@@ -297,9 +297,19 @@ template <typename T, int V, int NIN, int U, bool NTL, bool NT, class Op>
 __global__ __launch_bounds__(kThreads) void map_rows_kernel(MapPlan<NIN> p) {
   const uint32_t tile = blockIdx.x * (kThreads * U);
   const FastDiv& rows = p.div[0];  // vectors per row: size[0] / V
-  dev::scalar_here(p.out);
+  // the plan fields the loads need, in registers before the bounds test: one
+  // round of scalar loads (one asm statement: each is a scheduling boundary)
+  if constexpr (NIN == 1)
+    __asm__ volatile("" ::"s"(p.out), "s"(p.in[0]), "s"(rows.d), "s"(rows.mul), "s"(rows.shr), "s"(p.ostride[1]),
+                     "s"(p.istride[0][1]), "s"(p.units));
+  else if constexpr (NIN == 2)
+    __asm__ volatile("" ::"s"(p.out), "s"(p.in[0]), "s"(p.in[1]), "s"(rows.d), "s"(rows.mul), "s"(rows.shr),
+                     "s"(p.ostride[1]), "s"(p.istride[0][1]), "s"(p.istride[1][1]), "s"(p.units));
+  else {
+    dev::scalar_here(p.out);
 #pragma unroll
-  for (int k = 0; k < NIN; ++k) dev::scalar_here(p.in[k]);
+    for (int k = 0; k < NIN; ++k) dev::scalar_here(p.in[k]);
+  }
   VecT<T, V> raw[U][NIN];
   int32_t oo[U];
 #pragma unroll
