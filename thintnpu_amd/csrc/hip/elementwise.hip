@@ -992,6 +992,10 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(TransposePlan p) {
   constexpr uint32_t V = 16 / sizeof(T);
   constexpr uint32_t kRow = kTile + 4 / sizeof(T);  // padded LDS row, in elements
   __shared__ __attribute__((aligned(16))) T tile[W * kTile * kRow];
+  // the plan in registers before the first test of one of its fields: one
+  // round of scalar loads (one asm statement: each is a scheduling boundary)
+  __asm__ volatile("" ::"s"(p.src), "s"(p.dst), "s"(p.M), "s"(p.P), "s"(p.s_m), "s"(p.s_b), "s"(p.d_p), "s"(p.d_b),
+                   "s"(p.tiles_m), "s"(p.tiles_p), "s"(p.vec_src), "s"(p.vec_dst));
   const uint32_t tiles_p = p.tiles_p / W;  // blocks along p
   const uint32_t per_b = p.tiles_m * tiles_p;
   const uint32_t b = blockIdx.x / per_b, rest = blockIdx.x - b * per_b;

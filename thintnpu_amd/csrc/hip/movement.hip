@@ -968,6 +968,10 @@ struct PackPlan {
 template <bool NT>
 __global__ __launch_bounds__(kThreads) void pack_kernel(PackPlan p) {
   __shared__ uint16_t tile[16][kTile + 2];
+  // the plan in registers before the first test of one of its fields: one
+  // round of scalar loads (one asm statement: each is a scheduling boundary)
+  __asm__ volatile("" ::"s"(p.x), "s"(p.y), "s"(p.x_n), "s"(p.x_c), "s"(p.x_hw), "s"(p.y_n), "s"(p.y_c1),
+                   "s"(p.channels), "s"(p.c1), "s"(p.hw), "s"(p.tiles), "s"(p.vec_ok));
   const uint32_t t = blockIdx.x % p.tiles;
   const uint32_t plane = blockIdx.x / p.tiles;  // n * c1 + cb
   const uint32_t n = plane / p.c1, cb = plane - n * p.c1;
