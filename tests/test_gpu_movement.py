@@ -151,6 +151,26 @@ def test_upsample_streaming_block_windows(gpu):
         assert bits_equal(fused, mv.upsample_cat_blocked([o, x], [False, True])), (n, c1, h, w)
 
 
+@pytest.mark.parametrize("n", [1, 8])
+def test_upsample_cat_many_inputs(gpu, n):
+    """Three to six inputs (the general input-count form of the plane
+    kernel), upsampled and copied ones interleaved, an input with no channel
+    blocks among them and at the end; n=8 crosses the streaming size from
+    four inputs on."""
+    from thintnpu_amd import capi
+    h, w = 20, 24
+    specs = [(3, True), (2, False), (0, False), (4, True), (1, False), (0, True)]
+    parts, flags = [], []
+    for k, (c1, up) in enumerate(specs):
+        hh, ww = (h, w) if up else (2 * h, 2 * w)
+        parts.append(random_bits16((n, c1, hh, ww, 16), 500 + 10 * n + k))
+        flags.append(up)
+    for count in (3, 4, 6):
+        ps, fs = parts[:count], flags[:count]
+        got = capi.upsample_cat_nc1hwc0([p.to(gpu) for p in ps], fs).cpu()
+        assert bits_equal(got, mv.upsample_cat_blocked(ps, fs)), (n, count)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_upsample_nchw(gpu, dtype):
     """verify_all.py:88-94 shapes, atol 0."""
