@@ -345,6 +345,12 @@ __global__ __launch_bounds__(kThreads) void softmax_cols8_kernel(SoftmaxPlan p) 
   // in one L2.  The grid is a multiple of 8.
   const uint32_t logical = (blockIdx.x & 7u) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   uint32_t base = (logical * kWaves + (threadIdx.x >> 6)) * kSlots;  // wave-uniform
+  // the plan fields of the first two column dims in registers before the
+  // bounds tests: one round of scalar loads (one asm statement: each is a
+  // scheduling boundary)
+  __asm__ volatile("" ::"s"(p.x), "s"(p.out), "s"(p.xr), "s"(p.orr), "s"(p.units), "s"(p.nd), "s"(p.div[0].mul),
+                   "s"(p.div[0].shr), "s"(p.size[0]), "s"(p.xs[0]), "s"(p.os[0]), "s"(p.div[1].mul),
+                   "s"(p.div[1].shr), "s"(p.size[1]), "s"(p.xs[1]), "s"(p.os[1]));
   if (base >= p.units) return;
 
   auto load = [&](uint32_t u, h8 (&v)[RP]) {
