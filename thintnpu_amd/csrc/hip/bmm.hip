@@ -681,6 +681,11 @@ struct SelectPlan {
 };
 
 __global__ __launch_bounds__(256) void channel_select_kernel(SelectPlan p) {
+  // the plan in registers before the loop's bounds test: one round of scalar
+  // loads (one asm statement: each is a scheduling boundary)
+  __asm__ volatile("" ::"s"(p.x), "s"(p.y), "s"(p.xs1), "s"(p.xs2), "s"(p.xs3), "s"(p.ys1), "s"(p.ys2), "s"(p.ys3),
+                   "s"(p.tokens.d), "s"(p.tokens.mul), "s"(p.tokens.shr), "s"(p.count.d), "s"(p.count.mul),
+                   "s"(p.count.shr), "s"(p.group), "s"(p.begin), "s"(p.total));
   for (uint64_t e = (uint64_t)blockIdx.x * 256 + threadIdx.x; e < p.total; e += (uint64_t)gridDim.x * 256) {
     const uint32_t lane = (uint32_t)(e & 15u);
     const uint32_t rest = (uint32_t)(e >> 4);  // cb * T + t
