@@ -131,15 +131,42 @@ struct OpSilu {
     return from_f<T>(silu_f<T>(to_f(v[0])));
   }
 };
+// x / (1 + exp(-x)) in fp32 for an fp16 x, to the accuracy of the library expf
+// and an IEEE division, in about half their instructions:
+//   * exp(-x) = 2^n * 2^f.  t = x * -log2(e)_hi is exact (13 significant bits
+//     of log2(e) times the 11 of x), n = rint(t), f = (t - n) - x * log2(e)_lo
+//     (|f| <= 0.51, one rounding), 2^f by the hardware exp2, scaled by ldexp.
+//     x is first clamped to [-65504, 64]: exp(-64) already leaves 1 + e == 1,
+//     a NaN clamps to a number (the NaN comes back through x below), and n
+//     stays finite.
+//   * x / d, d = 1 + e: q0 = x * rcp(d), one Newton step q0 + rcp(d)(x - q0 d)
+//     (the residual exact through fma), then v_div_fixup_f32 for the special
+//     operands: d = inf gives a zero of x's sign (x <= -88.7, as x / inf), or
+//     NaN for x = -inf; x = +inf gives +inf; a NaN x stays NaN.
+__device__ __forceinline__ float silu_f16_accurate(float x) {
+  constexpr float kL2eHi = 1.442626953125f;       // log2(e) truncated to 13 significant bits
+  constexpr float kL2eLo = 6.8087763963387e-05f;  // log2(e) - kL2eHi
+  const float xe = fmaxf(fminf(x, 64.0f), -65504.0f);
+  const float t = xe * -kL2eHi;
+  const float n = __builtin_rintf(t);
+  const float e = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f(__builtin_fmaf(xe, -kL2eLo, t - n)), (int)n);
+  const float d = 1.0f + e;
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q0 = x * r;
+  return __builtin_amdgcn_div_fixupf(__builtin_fmaf(__builtin_fmaf(-q0, d, x), r, q0), d, x);
+}
+
 // y + silu(x), one rounding.  The residual add can cancel (y ~ -silu(x)), which
-// magnifies any fp32 error of silu(x) relative to the small result, so this op
-// evaluates silu with the library expf and IEEE division -- the same formula and
-// accuracy class as PyTorch CPU's fp32 x / (1 + exp(-x)).
+// magnifies any fp32 error of silu(x) relative to the small result, so silu
+// is evaluated to the accuracy class of PyTorch CPU's fp32 x / (1 + exp(-x)):
+// library expf and IEEE division for fp32 tensors, silu_f16_accurate (the
+// same steps, specialised to an fp16 operand) for fp16 ones.
 struct OpSiluAdd {
   template <typename T, int NIN>
   __device__ __forceinline__ T operator()(const T (&v)[NIN], float, float) const {
-    float x = to_f(v[0]);
-    return from_f<T>(to_f(v[1]) + x / (1.0f + expf(-x)));
+    const float x = to_f(v[0]);
+    if constexpr (std::is_same<T, _Float16>::value) return from_f<T>(to_f(v[1]) + silu_f16_accurate(x));
+    else return from_f<T>(to_f(v[1]) + x / (1.0f + expf(-x)));
   }
 };
 // silu(round(round(x*s) + b)): the fp16 roundings of the unfused chain.
