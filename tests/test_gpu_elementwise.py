@@ -241,6 +241,22 @@ def test_silu_add_c1(gpu, n):
     assert rep["cancel_only"] <= C1_CANCEL_ONLY[n][0] and rep["cancel_max_ulp"] <= C1_CANCEL_ONLY[n][1]
 
 
+def test_silu_add_all_encodings(gpu):
+    """y + SiLU(x) for every fp16 encoding of x against each special y (signed
+    zeros, infinities, NaN, extremes, subnormals) and a random y: the fp16
+    SiLU's argument split, Newton quotient and special-operand fix-up (x <=
+    -88.7 where exp(-x) overflows, x = -inf -> NaN, x = +inf -> +inf) within
+    the fused bound, NaNs and infinities where the oracle has them."""
+    from thintnpu_amd import capi
+    x_all = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    ys = list(specials16()) + [random_bits16((65536,), 21)]
+    x = x_all.repeat(len(ys))
+    y = torch.cat([yv.expand(65536) if yv.dim() == 0 else yv for yv in ys]).contiguous()
+    got = capi.silu_add(x.to(gpu), y.to(gpu)).cpu()
+    rep = assert_fused_cancel(got, ew.silu_add(x, y), ew.silu(x.float()), 2, 4, "silu_add encodings")
+    assert rep["exact"] > 0.999 * rep["finite"]
+
+
 C2_SHAPES = [(128, 80, 80), (256, 40, 40), (512, 20, 20)]
 
 
