@@ -543,8 +543,8 @@ struct DecodePlan {
   uint32_t score_units;   // B * nc * svecs
   FastDiv div_apairs, div_svecs, div_nc;
   int32_t xywh;
-  int32_t direct;         // boxes are the distances themselves (reg_max = 1 heads)
   uint32_t boxes_bytes;   // byte extent of boxes from its base (buffer-load forms)
+  int32_t direct;         // boxes are the distances themselves (reg_max = 1 heads)
 };
 
 __device__ __forceinline__ _Float16 h_from_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
@@ -559,20 +559,26 @@ constexpr uint32_t kDecodeScoreUnits = VS == 8 ? 2u : 1u;
 // output stores (launches of at least kStreamingBytes).
 template <int VB, int VS, int LOAD>
 __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
-  // The score role's plan fields (most blocks take that role) in registers
-  // before the test of the role: they then load in the same round of scalar
-  // loads as p.box_blocks, not in two more behind it.
-  // (One statement: each inline asm is a scheduling boundary of its own.)
+  // Both roles' plan fields in registers before the test of the role: they
+  // then load in the same round of scalar loads as p.box_blocks, not in two
+  // or three more behind it.  (One statement: each inline asm is a
+  // scheduling boundary of its own.)
   __asm__ volatile("" ::"s"(p.scores), "s"(p.out), "s"(p.sb), "s"(p.sc), "s"(p.sa), "s"(p.ob), "s"(p.oc),
                    "s"(p.oa), "s"(p.score_units), "s"(p.svecs), "s"(p.nc), "s"(p.div_svecs.mul),
-                   "s"(p.div_svecs.shr), "s"(p.div_nc.mul), "s"(p.div_nc.shr), "s"(p.box_blocks));
+                   "s"(p.div_svecs.shr), "s"(p.div_nc.mul), "s"(p.div_nc.shr), "s"(p.box_blocks), "s"(p.boxes),
+                   "s"(p.bb), "s"(p.bc), "s"(p.ba), "s"(p.boxes_bytes), "s"(p.box_units), "s"(p.apairs),
+                   "s"(p.div_apairs.mul), "s"(p.div_apairs.shr), "s"(p.xywh), "s"(p.levels), "s"(p.direct));
   if (blockIdx.x < p.box_blocks) {
     const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
     if (u >= p.box_units) return;
     const uint32_t ba_ = p.div_apairs.div(u);          // b * 2 + axis
     const uint32_t a0 = (u - ba_ * p.apairs) * VB;
     const uint32_t b = ba_ >> 1, axis = ba_ & 1u;
-    _Float16 bins[16][VB];
+    // Both sides' bins are loaded before either is reduced, and the anchors'
+    // level, centre and stride (plan fields only) are worked out under those
+    // loads: one memory round trip per thread instead of two, and the level
+    // search off the path after it.
+    _Float16 bins[16][VB], bins_hi[16][VB];
     float lo[VB], hi[VB];
     if (p.direct) {
       // distances as they are: the lt / rb channels of this axis
@@ -594,17 +600,13 @@ __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
       const uint32_t bc = 2u * (uint32_t)p.bc;
       const uint32_t off = 2u * (b * (uint32_t)p.bb + a0 * (uint32_t)p.ba) + axis * 16u * bc;
       dev::dfl_load_buffer<VB, LOAD == 2>(rs, off, bc, bins);
-      dev::dfl_side<VB, true>(bins, lo);
-      dev::dfl_load_buffer<VB, LOAD == 2>(rs, off + 32u * bc, bc, bins);
-      dev::dfl_side<VB, true>(bins, hi);
+      dev::dfl_load_buffer<VB, LOAD == 2>(rs, off + 32u * bc, bc, bins_hi);
     } else {
       const char* xc = reinterpret_cast<const char*>(p.boxes + b * p.bb + (int64_t)a0 * p.ba);
       dev::dfl_load<VB>(xc, 2 * (uint64_t)((int64_t)(axis * 16) * p.bc), 2 * (uint64_t)p.bc, bins);
-      dev::dfl_side<VB, true>(bins, lo);
-      dev::dfl_load<VB>(xc, 2 * (uint64_t)((int64_t)((axis + 2) * 16) * p.bc), 2 * (uint64_t)p.bc, bins);
-      dev::dfl_side<VB, true>(bins, hi);
+      dev::dfl_load<VB>(xc, 2 * (uint64_t)((int64_t)((axis + 2) * 16) * p.bc), 2 * (uint64_t)p.bc, bins_hi);
     }
-    _Float16 first[VB], second[VB];
+    _Float16 centre[VB], stride[VB];
 #pragma unroll
     for (int j = 0; j < VB; ++j) {
       const uint32_t a = a0 + j;
@@ -612,16 +614,24 @@ __global__ __launch_bounds__(kThreads) void detect_decode_kernel(DecodePlan p) {
       while (l + 1 < p.levels && a >= p.start[l + 1]) ++l;
       const uint32_t local = a - p.start[l];
       const uint32_t y = p.width[l].div(local), x = local - y * p.width[l].d;
-      const _Float16 centre = (_Float16)(float)(axis ? y : x) + (_Float16)0.5f;
-      const _Float16 stride = h_from_bits(p.stride_bits[l]);
-      const _Float16 lower = centre - (_Float16)lo[j];
-      const _Float16 upper = centre + (_Float16)hi[j];
+      centre[j] = (_Float16)(float)(axis ? y : x) + (_Float16)0.5f;
+      stride[j] = h_from_bits(p.stride_bits[l]);
+    }
+    if (!p.direct) {
+      dev::dfl_side<VB, true>(bins, lo);
+      dev::dfl_side<VB, true>(bins_hi, hi);
+    }
+    _Float16 first[VB], second[VB];
+#pragma unroll
+    for (int j = 0; j < VB; ++j) {
+      const _Float16 lower = centre[j] - (_Float16)lo[j];
+      const _Float16 upper = centre[j] + (_Float16)hi[j];
       if (p.xywh) {
-        first[j] = ((lower + upper) / (_Float16)2.0f) * stride;
-        second[j] = (upper - lower) * stride;
+        first[j] = ((lower + upper) / (_Float16)2.0f) * stride[j];
+        second[j] = (upper - lower) * stride[j];
       } else {
-        first[j] = lower * stride;
-        second[j] = upper * stride;
+        first[j] = lower * stride[j];
+        second[j] = upper * stride[j];
       }
     }
     _Float16* o = p.out + b * p.ob + (int64_t)a0 * p.oa;
