@@ -97,6 +97,9 @@ __global__ __launch_bounds__(kThreads) void softmax_row_kernel(SoftmaxPlan p) {
   const uint32_t g = lane % G;
   const uint32_t row = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * RPW + lane / G;
   const bool live = row < p.units;  // every lane still joins the group shuffles
+  // the operand pointers in registers with the first round of scalar loads
+  // (they were loaded only after the test of p.nd in col_offsets)
+  __asm__ volatile("" ::"s"(p.x), "s"(p.out), "s"(p.units), "s"(p.nd), "s"(p.R));
   // offsets of a clamped row rather than under a test of live, so that the
   // plan's scalar loads are not held behind the load of p.units
   int64_t xo, oo;
@@ -133,15 +136,20 @@ __global__ __launch_bounds__(kThreads) void softmax_row_kernel(SoftmaxPlan p) {
   }
   struct alignas(VE * sizeof(TI)) WI { TI e[VE]; };
   WI raw[KPT];
+  // every chunk's load issued, unconditionally (chunks past the row reload
+  // its last one, unused), before the first is used: one memory round trip
+  // per row, not one per chunk
+#pragma unroll
+  for (int k = 0; k < KPT; ++k) {
+    const WI* src = reinterpret_cast<const WI*>(xr) + min(g + G * k, chunks - 1);
+    if constexpr (VEC && NT) raw[k] = __builtin_bit_cast(WI, __builtin_nontemporal_load(
+                                 reinterpret_cast<const uint32_t __attribute__((ext_vector_type(4)))*>(src)));
+    else raw[k] = *src;
+  }
   float m = -__builtin_inff();
 #pragma unroll
   for (int k = 0; k < KPT; ++k) {
-    const uint32_t c = g + G * k;
-    if (live && c < chunks) {
-      const WI* src = reinterpret_cast<const WI*>(xr) + c;
-      if constexpr (VEC && NT) raw[k] = __builtin_bit_cast(WI, __builtin_nontemporal_load(
-                                   reinterpret_cast<const uint32_t __attribute__((ext_vector_type(4)))*>(src)));
-      else raw[k] = *src;
+    if (live && g + G * k < chunks) {
 #pragma unroll
       for (int j = 0; j < VE; ++j) m = fmaxf(m, (float)raw[k].e[j]);
     }
