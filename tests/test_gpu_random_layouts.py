@@ -1,7 +1,7 @@
 """Seeded random layouts through the C ABI: permuted, sliced, stepped and
 broadcast views of fp16 / fp32 tensors, non-contiguous outputs, and the
-binary and unary ops, strided copy and concatenation on them, each against
-the oracle.
+binary and unary ops, strided copy, concatenation and softmax on them, each
+against the oracle.
 The fixed shapes of the other tests pin the paths the model takes; these
 exercise the dimension coalescing and kernel selection on layouts that no
 fixed case names."""
@@ -142,3 +142,22 @@ def test_unary_random_views(gpu, dtype):
                 assert_ulp(got, ref(xc), 2, what)
             else:
                 torch.testing.assert_close(got, ref(xc), rtol=1e-5, atol=1e-6, msg=what)
+
+
+@pytest.mark.parametrize("half_to_float", [False, True])
+def test_softmax_random_views(gpu, half_to_float):
+    """fp16 softmax over a random dim of a random view (row, column, short
+    column and stream forms alike), to the bars of the softmax tests."""
+    from tests.test_gpu_softmax import check_softmax
+    from thintnpu_amd import capi
+    rng = random.Random(31337 + half_to_float)
+    sizes = SIZES + [64, 400, 2048]
+    for case in range(40):
+        rank = rng.randint(1, 4)
+        shape = [rng.choice(sizes if rng.random() < 0.3 else SIZES) for _ in range(rank)]
+        while torch.Size(shape).numel() > (1 << 20):
+            shape[rng.randrange(rank)] = rng.choice(SIZES)
+        dim = rng.randrange(rank)
+        xc, xg = random_view(rng, shape, torch.float16, gpu, 5 * case + 11)
+        got = capi.softmax(xg, dim, half_to_float).cpu()
+        check_softmax(got, xc, dim, half_to_float, f"case {case} dim {dim} {shape}/{list(xc.stride())}")
