@@ -15,6 +15,8 @@ from oracle import movement as mv
 from oracle.numerics import assert_ulp
 from tests.helpers import gen
 
+pytestmark = pytest.mark.gpu
+
 SIZES = [1, 2, 3, 5, 7, 8, 9, 16, 17, 33]
 BITS = {torch.float16: torch.int16, torch.float32: torch.int32}
 
