@@ -58,6 +58,7 @@ struct BmmPlan {
   // streamed b: bytes from b.p to the end of its storage, vectors per
   // contiguous run along k (0 = one run) and the byte jump after a run
   uint32_t b_bytes, b_vrun, b_vjump;
+  FastDiv div_mt, div_nt;  // streamed form: block index -> (batch, row tile, column tile)
 };
 
 // Output tile of 4 * RM rows x 64 columns per block.  A and B are staged as
@@ -163,10 +164,8 @@ __global__ __launch_bounds__(64) void bmm_stream_kernel(BmmPlan p) {
   __shared__ __attribute__((aligned(16))) float As[RM][kDepth];
   const uint32_t lane = threadIdx.x;
   uint32_t t = blockIdx.x;
-  const uint32_t nt = t % p.ntiles;
-  t /= p.ntiles;
-  const uint32_t mt = t % p.mtiles;
-  const uint32_t bt = t / p.mtiles;
+  const uint32_t q = p.div_nt.div(t), nt = t - q * p.ntiles;  // no integer division sequence
+  const uint32_t bt = p.div_mt.div(q), mt = q - bt * p.mtiles;
   const uint32_t i0 = mt * RM, j = nt * kBmmCols + lane;
   const _Float16* bcol = p.b.p + (int64_t)bt * p.b.batch +
                          p.b.col.at(min(j, p.n - 1) + p.b.col_origin + bt * p.b.col_group);
@@ -636,6 +635,8 @@ extern "C" thin_status thin_layout_bmm(const thin_desc* a, const thin_desc* b, c
     auto waves = [&](int rm) { return (uint64_t)s.batch * ((s.m + rm - 1) / rm) * p.ntiles; };
     const int rm = waves(2) < 512 ? 1 : waves(2) > 8192 ? 4 : 2;
     p.mtiles = (uint32_t)((s.m + rm - 1) / rm);
+    p.div_mt = FastDiv::make(p.mtiles);
+    p.div_nt = FastDiv::make(p.ntiles);
     const uint64_t grid = waves(rm);
     THIN_REQUIRE(grid < ((uint64_t)1 << 31), THIN_ERR_UNSUPPORTED, "bmm: too many output tiles");
     if (rm == 4)
