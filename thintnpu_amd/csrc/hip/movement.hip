@@ -965,8 +965,9 @@ struct PackPlan {
   uint32_t channels;        // C
   uint32_t c1;              // C1 = ceil(C/16)
   uint32_t hw;              // pixels per plane
-  uint32_t tiles;           // ceil(hw / kTile)
+  uint32_t tiles;           // ceil(hw / tile pixels)
   uint32_t vec_ok;          // pixel rows 16-byte aligned and dense
+  FastDiv div_tiles, div_c1;  // block index -> (n, c1 block, tile) with no integer division sequence
 };
 
 // pack: NCHW -> NC1HWC0 (zero-fill channels >= C), TILE pixels a block
@@ -976,10 +977,10 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackPlan p) {
   // the plan in registers before the first test of one of its fields: one
   // round of scalar loads (one asm statement: each is a scheduling boundary)
   __asm__ volatile("" ::"s"(p.x), "s"(p.y), "s"(p.x_n), "s"(p.x_c), "s"(p.x_hw), "s"(p.y_n), "s"(p.y_c1),
-                   "s"(p.channels), "s"(p.c1), "s"(p.hw), "s"(p.tiles), "s"(p.vec_ok));
-  const uint32_t t = blockIdx.x % p.tiles;
-  const uint32_t plane = blockIdx.x / p.tiles;  // n * c1 + cb
-  const uint32_t n = plane / p.c1, cb = plane - n * p.c1;
+                   "s"(p.channels), "s"(p.c1), "s"(p.hw), "s"(p.tiles), "s"(p.vec_ok), "s"(p.div_tiles.mul),
+                   "s"(p.div_tiles.shr), "s"(p.div_c1.mul), "s"(p.div_c1.shr));
+  const uint32_t plane = p.div_tiles.div(blockIdx.x), t = blockIdx.x - plane * p.tiles;  // plane = n * c1 + cb
+  const uint32_t n = p.div_c1.div(plane), cb = plane - n * p.c1;
   const uint32_t pix0 = t * TILE;
   const uint32_t count = min((uint32_t)TILE, p.hw - pix0);
   // load: 16 channel rows x count pixels
@@ -1029,9 +1030,8 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(PackPlan p) {
 // unpack: NC1HWC0 -> NCHW for channels < C
 __global__ __launch_bounds__(kThreads) void unpack_kernel(PackPlan p) {
   __shared__ uint16_t tile[16][kTile + 2];
-  const uint32_t t = blockIdx.x % p.tiles;
-  const uint32_t plane = blockIdx.x / p.tiles;
-  const uint32_t n = plane / p.c1, cb = plane - n * p.c1;
+  const uint32_t plane = p.div_tiles.div(blockIdx.x), t = blockIdx.x - plane * p.tiles;
+  const uint32_t n = p.div_c1.div(plane), cb = plane - n * p.c1;
   const uint32_t pix0 = t * kTile;
   const uint32_t count = min((uint32_t)kTile, p.hw - pix0);
   const uint16_t* xp = p.y + n * p.y_n + (int64_t)cb * p.y_c1 + (int64_t)pix0 * 16;  // y holds the blocked source
@@ -1137,6 +1137,8 @@ thin_status repack(const thin_desc* nchw, const thin_desc* blocked, bool to_bloc
   p.tiles = (p.hw + tile_px - 1) / tile_px;
   const uint64_t blocks = (uint64_t)n * c1 * p.tiles;
   THIN_REQUIRE(blocks < (1ull << 31), THIN_ERR_UNSUPPORTED, "repack: too many tiles");
+  p.div_tiles = FastDiv::make(p.tiles);
+  p.div_c1 = FastDiv::make(p.c1);
   const bool nt = n * c1 * h * w * 32 >= kStreamingBytes;
   if (wide && nt)
     hipLaunchKernelGGL((pack_kernel<true, kWideTile>), dim3((uint32_t)blocks), dim3(kThreads), 0, stream, p);
