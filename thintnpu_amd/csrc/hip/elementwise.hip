@@ -135,7 +135,8 @@ struct OpSilu {
 // and an IEEE division, in about half their instructions:
 //   * exp(-x) = 2^n * 2^f.  t = x * -log2(e)_hi is exact (13 significant bits
 //     of log2(e) times the 11 of x), n = rint(t), f = (t - n) - x * log2(e)_lo
-//     (|f| <= 0.51, one rounding), 2^f by the hardware exp2, scaled by ldexp.
+//     (one rounding; |f| <= 0.51 wherever e is finite), 2^f by the hardware
+//     exp2, scaled by ldexp.
 //     x is first clamped to [-65504, 64]: exp(-64) already leaves 1 + e == 1,
 //     a NaN clamps to a number (the NaN comes back through x below), and n
 //     stays finite.
