@@ -347,6 +347,22 @@ def test_maxpool_wide_rows(gpu, c, h, w, k):
     check_pool(capi.maxpool2d_nchw(y.to(gpu), k).cpu(), mv.maxpool_nchw(y, k), f"nchw {h}x{w * 5} k{k}")
 
 
+@pytest.mark.parametrize("k", [3, 5])
+def test_maxpool_band_and_register_forms(gpu, k):
+    """Planes too large for the whole-plane kernel: bands of rows staged in
+    LDS (a 72x72 NC1HWC0 plane, through both the packed maximum and the
+    first-maximum selects), and the register window for rows too wide for a
+    band of 2R + 1 rows (520 pixels NC1HWC0, 8200 NCHW)."""
+    from thintnpu_amd import capi
+    band = to_blocked(normal16((2, 32, 72, 72), 70 + k))
+    for what, x in (("band, +0/-0 ties", pool_specials(band)), ("band, packed", pool_specials_packed(band, 0.0, 90 + k))):
+        check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"{what} k{k}")
+    x = pool_specials(to_blocked(normal16((1, 16, 8, 520), 60 + k)))
+    check_pool(capi.maxpool_nc1hwc0(x.to(gpu), k).cpu(), mv.maxpool_blocked(x, k), f"register 8x520 k{k}")
+    y = pool_specials(normal16((1, 2, 5, 8200), 50 + k))
+    check_pool(capi.maxpool2d_nchw(y.to(gpu), k).cpu(), mv.maxpool_nchw(y, k), f"nchw register 5x8200 k{k}")
+
+
 def test_cat_beyond_4gib(gpu):
     """A cat whose output passes 4 GiB (the second input lands 2 GiB in): the
     row and column offsets are 64-bit.  Small integers make torch.cat on the

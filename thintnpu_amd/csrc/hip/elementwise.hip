@@ -466,11 +466,12 @@ __global__ __launch_bounds__(kThreads) void affine_silu_blocked_kernel(AffinePla
     const h8v bv = *reinterpret_cast<const h8v*>(p.b + n * p.b_n + c1 * p.b_c1 + half * 8);
     for (uint32_t tile = blockIdx.x * kThreads * U; tile < p.plane_vecs;
          tile += gridDim.x * kThreads * U) {
+      // every load issued (clamped into the plane) before the first is used
       h8v xv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const uint32_t v = tile + u * kThreads + threadIdx.x;
-        if (v < p.plane_vecs) xv[u] = *reinterpret_cast<const h8v*>(xp + (size_t)v * 8);
+        const uint32_t v = min(tile + u * kThreads + threadIdx.x, p.plane_vecs - 1);
+        xv[u] = *reinterpret_cast<const h8v*>(xp + (size_t)v * 8);
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -1079,18 +1080,37 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(TransposePlan p) {
     }
   }
   if constexpr (W == 1) {
-  // load: tile row r = m0 + r, columns p0 .. p0+63
-  for (uint32_t i = threadIdx.x; i < kTile * kTile / V; i += kThreads) {
-    const uint32_t r = i / (kTile / V), cv = (i % (kTile / V)) * V;
-    const T* row = src + (int64_t)(m0 + r) * p.s_m + p0 + cv;
-    if (full && p.vec_src) {
-      const VecT<T, V> w = load16<NT, VecT<T, V>>(row);
+  // load: tile row r = m0 + r, columns p0 .. p0+63; every load of the thread
+  // issued before the first LDS write (a partial tile loads each element
+  // from a position clamped into the matrix and writes only those inside)
+  constexpr uint32_t U = kTile * kTile / V / kThreads;
+  VecT<T, V> w[U];
+  if (full && p.vec_src) {
 #pragma unroll
-      for (uint32_t j = 0; j < V; ++j) tile[r * kRow + cv + j] = w.v[j];
-    } else {
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = threadIdx.x + u * kThreads, r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+      w[u] = load16<NT, VecT<T, V>>(src + (int64_t)(m0 + r) * p.s_m + p0 + cv);
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = threadIdx.x + u * kThreads, r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+#pragma unroll
+      for (uint32_t j = 0; j < V; ++j) tile[r * kRow + cv + j] = w[u].v[j];
+    }
+  } else {
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = threadIdx.x + u * kThreads, r = i / (kTile / V), cv = (i % (kTile / V)) * V;
+      const T* row = src + (int64_t)min(m0 + r, p.M - 1) * p.s_m;
+#pragma unroll
+      for (uint32_t j = 0; j < V; ++j) w[u].v[j] = row[min(p0 + cv + j, p.P - 1)];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < U; ++u) {
+      const uint32_t i = threadIdx.x + u * kThreads, r = i / (kTile / V), cv = (i % (kTile / V)) * V;
 #pragma unroll
       for (uint32_t j = 0; j < V; ++j)
-        if (m0 + r < p.M && p0 + cv + j < p.P) tile[r * kRow + cv + j] = row[j];
+        if (m0 + r < p.M && p0 + cv + j < p.P) tile[r * kRow + cv + j] = w[u].v[j];
     }
   }
   __syncthreads();

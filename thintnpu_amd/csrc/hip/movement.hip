@@ -530,16 +530,24 @@ __global__ __launch_bounds__(kThreads) void maxpool_kernel(PoolPlan p) {
   PoolVec<T, V> ninf;
 #pragma unroll
   for (int j = 0; j < V; ++j) ninf.e[j] = (T)(-__builtin_inff());
-  // horizontal max of input row yy at column x (-inf outside the plane)
+  // horizontal max of input row yy at column x (-inf outside the plane):
+  // the K taps are loaded unconditionally from positions clamped into the
+  // plane, all in flight before the first is used, and a tap outside the
+  // plane is skipped (as an -inf tap would be)
   auto hmax = [&](int yy) {
-    PoolVec<T, V> m = ninf;
-    if (yy >= 0 && yy < (int)p.h) {
-      const T* row = xp + (int64_t)yy * p.xs[2];
+    const bool row_ok = yy >= 0 && yy < (int)p.h;
+    const T* row = xp + (int64_t)min(max(yy, 0), (int)p.h - 1) * p.xs[2];
+    PoolVec<T, V> t[K];
 #pragma unroll
-      for (int dx = -R; dx <= R; ++dx) {
-        const int xx = (int)x + dx;
-        if (xx >= 0 && xx < (int)p.w) keep_max(m, *reinterpret_cast<const PoolVec<T, V>*>(row + (int64_t)xx * p.xs[3]));
-      }
+    for (int i = 0; i < K; ++i) {
+      const int xx = min(max((int)x + i - R, 0), (int)p.w - 1);
+      t[i] = *reinterpret_cast<const PoolVec<T, V>*>(row + (int64_t)xx * p.xs[3]);
+    }
+    PoolVec<T, V> m = ninf;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int xx = (int)x + i - R;
+      if (row_ok && xx >= 0 && xx < (int)p.w) keep_max(m, t[i]);
     }
     return m;
   };
@@ -596,32 +604,45 @@ __global__ __launch_bounds__(kThreads) void maxpool_tile_kernel(PoolPlan p, uint
   // per-thread minima of the loaded bits and of the bits with the sign
   // flipped: a zero lane means the tile holds a +0 (resp. a -0)
   u16x8 min_pos = (u16x8)(uint16_t)0xffff, min_neg = (u16x8)(uint16_t)0xffff;
-  // four loads in flight per thread before their LDS writes
+  // four loads in flight per thread before their LDS writes.  The packed
+  // form, which uses each loaded vector for its zero-sign minima, issues its
+  // loads unconditionally from positions clamped into the plane and replaces
+  // a pixel outside the plane (or past the tile) by -inf afterwards: a load
+  // under a branch and used inside it is waited for before the next load is
+  // issued.  The other forms load under the branch and use nothing there.
   constexpr int U = 4;
   for (uint32_t i0 = threadIdx.x; i0 < tile; i0 += U * kThreads) {
     PV v[U];
+    bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t i = i0 + u * kThreads;
-      v[u] = ninf;
-      if (i < tile) {
-        const uint32_t rr = p.div_prow.div(i), k = i - rr * prow;
-        const int x = (int)(k >> pshift) - R;
-        const uint32_t part = k & pshift;
-        const int yy = y0 - R + (int)rr;
-        if (yy >= 0 && yy < (int)p.h && x >= 0 && x < (int)p.w) {
-          v[u] = *reinterpret_cast<const PV*>(xp + (int64_t)yy * p.xs[2] + (int64_t)x * p.xs[3] + (int64_t)part * V);
-          if constexpr (kPacked) {
-            const u16x8 b = __builtin_bit_cast(u16x8, v[u]);
-            min_pos = __builtin_elementwise_min(min_pos, b);
-            min_neg = __builtin_elementwise_min(min_neg, b ^ (uint16_t)0x8000);
-          }
-        }
+      const uint32_t rr = p.div_prow.div(i), k = i - rr * prow;
+      const int x = (int)(k >> pshift) - R;
+      const uint32_t part = k & pshift;
+      const int yy = y0 - R + (int)rr;
+      ok[u] = i < tile && yy >= 0 && yy < (int)p.h && x >= 0 && x < (int)p.w;
+      if constexpr (kPacked) {
+        const int yc = min(max(yy, 0), (int)p.h - 1), xc = min(max(x, 0), (int)p.w - 1);
+        v[u] = *reinterpret_cast<const PV*>(xp + (int64_t)yc * p.xs[2] + (int64_t)xc * p.xs[3] + (int64_t)part * V);
+      } else {
+        v[u] = ninf;
+        if (ok[u]) v[u] = *reinterpret_cast<const PV*>(xp + (int64_t)yy * p.xs[2] + (int64_t)x * p.xs[3] + (int64_t)part * V);
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+      if constexpr (kPacked) {
+        if (!ok[u]) {
+          v[u] = ninf;
+        } else {
+          const u16x8 b = __builtin_bit_cast(u16x8, v[u]);
+          min_pos = __builtin_elementwise_min(min_pos, b);
+          min_neg = __builtin_elementwise_min(min_neg, b ^ (uint16_t)0x8000);
+        }
+      }
       if (i0 + u * kThreads < tile) in[i0 + u * kThreads] = v[u];
+    }
   }
   bool exact = !kPacked;
   if constexpr (kPacked) {
