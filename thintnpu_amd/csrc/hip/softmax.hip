@@ -200,8 +200,22 @@ __global__ __launch_bounds__(kThreads) void softmax_row_stream_kernel(SoftmaxPla
   const TI* xr = static_cast<const TI*>(p.x) + xo;
   TO* orow = static_cast<TO*>(p.out) + oo;
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  // one pass over the thread's elements i = tid + k * kThreads, eight at a
+  // time: all eight loads (clamped into the row) issued before the first is
+  // used, the elements then taken in order
+  constexpr uint32_t B = 8;
+  auto pass = [&](auto&& f) {
+    for (uint32_t i0 = threadIdx.x; i0 < p.R; i0 += B * kThreads) {
+      float v[B];
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k) v[k] = ldf(xr + min(i0 + k * kThreads, p.R - 1));
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k)
+        if (i0 + k * kThreads < p.R) f(i0 + k * kThreads, v[k]);
+    }
+  };
   float m = -__builtin_inff();
-  for (uint32_t i = threadIdx.x; i < p.R; i += kThreads) m = max_nan(m, ldf(xr + i));
+  pass([&](uint32_t, float v) { m = max_nan(m, v); });
   m = wave_max_nan(m);
   if (lane == 0) red[wave] = m;
   __syncthreads();
@@ -210,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void softmax_row_stream_kernel(SoftmaxPla
   for (uint32_t w = 1; w < kWaves; ++w) m = max_nan(m, red[w]);
   __syncthreads();
   float s = 0.f;
-  for (uint32_t i = threadIdx.x; i < p.R; i += kThreads) s += expo<FAST>(ldf(xr + i) - m);
+  pass([&](uint32_t, float v) { s += expo<FAST>(v - m); });
   s = wave_sum(s);
   if (lane == 0) red[wave] = s;
   __syncthreads();
@@ -218,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void softmax_row_stream_kernel(SoftmaxPla
 #pragma unroll
   for (uint32_t w = 0; w < kWaves; ++w) s += red[w];
   const float inv = 1.0f / s;
-  for (uint32_t i = threadIdx.x; i < p.R; i += kThreads) stf(orow + i, expo<FAST>(ldf(xr + i) - m) * inv);
+  pass([&](uint32_t i, float v) { stf(orow + i, expo<FAST>(v - m) * inv); });
 }
 
 // ---------------------------------------------------------------- columns
@@ -299,23 +313,34 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
     }
     return;
   }
-  for (uint32_t r = 0; r < p.R; ++r) {
-    WI w = *reinterpret_cast<const WI*>(xc + r * p.xr);
+  // longer columns: three passes, each over the rows eight at a time with
+  // all eight loads (clamped into the column) issued before the first is
+  // used, the rows then taken in order
+  constexpr uint32_t B = 8;
+  auto pass = [&](auto&& f) {
+    for (uint32_t r0 = 0; r0 < p.R; r0 += B) {
+      WI w[B];
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k) w[k] = *reinterpret_cast<const WI*>(xc + (int64_t)min(r0 + k, p.R - 1) * p.xr);
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k)
+        if (r0 + k < p.R) f(r0 + k, w[k]);
+    }
+  };
+  pass([&](uint32_t, const WI& w) {
 #pragma unroll
     for (int j = 0; j < V; ++j) m[j] = max_nan(m[j], (float)w.e[j]);
-  }
-  for (uint32_t r = 0; r < p.R; ++r) {
-    WI w = *reinterpret_cast<const WI*>(xc + r * p.xr);
+  });
+  pass([&](uint32_t, const WI& w) {
 #pragma unroll
     for (int j = 0; j < V; ++j) s[j] += expd<FAST>((float)w.e[j], m[j]);
-  }
-  for (uint32_t r = 0; r < p.R; ++r) {
-    WI w = *reinterpret_cast<const WI*>(xc + r * p.xr);
+  });
+  pass([&](uint32_t r, const WI& w) {
     WO o;
 #pragma unroll
     for (int j = 0; j < V; ++j) o.e[j] = (TO)(expd<FAST>((float)w.e[j], m[j]) / s[j]);
-    *reinterpret_cast<WO*>(oc + r * p.orr) = o;
-  }
+    *reinterpret_cast<WO*>(oc + (int64_t)r * p.orr) = o;
+  });
 }
 
 // Short fp16 column reductions (R <= 16 rows) over 16-byte column groups: the
