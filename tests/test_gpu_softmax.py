@@ -215,6 +215,28 @@ def test_softmax_row_widths(gpu):
         check_softmax(run(capi, x.to(gpu), 1), x, 1, what=f"tiles {rows}x{width}")
 
 
+@pytest.mark.parametrize("half_to_float", [False, True])
+def test_softmax_long_columns(gpu, half_to_float):
+    """Reductions of more than 16 (vector units) or 32 (single columns) rows
+    over a non-innermost dim: few units, whose rows split over the slices of
+    a block (16-byte units, and unaligned single columns with a partial last
+    block of units), and enough units for one thread per unit; NaN, +inf, an
+    all -inf column and a large shift among them; long rows of both kinds."""
+    from thintnpu_amd import capi
+    for shape in ((8, 400, 400), (3, 100, 37), (2, 33, 24), (1, 24, 524288)):
+        x = normal16(shape, sum(shape) + half_to_float, std=3.0)
+        x[0, 3, 5] = float("nan")
+        x[0, 7, 6] = float("inf")
+        x[-1, :, 1] = float("-inf")
+        x[-1, 2, 2] += 10000
+        check_softmax(run(capi, x.to(gpu), 1, half_to_float), x, 1, half_to_float, what=f"long columns {shape}")
+    for width in (8400, 8401):
+        x = normal16((5, width), width, std=3.0)
+        x[1, 77] = float("nan")
+        x[2] = float("-inf")
+        check_softmax(run(capi, x.to(gpu), 1, half_to_float), x, 1, half_to_float, what=f"long rows {width}")
+
+
 def test_softmax_short_columns(gpu):
     """Reductions of <= 16 rows whose columns run contiguous in the innermost
     dim (the DFL bin softmax layout), staged through LDS tiles: reductions

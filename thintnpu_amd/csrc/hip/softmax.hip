@@ -343,6 +343,89 @@ __global__ __launch_bounds__(kThreads) void softmax_col_kernel(SoftmaxPlan p) {
   });
 }
 
+// Long columns (R > 16) when there are too few column units to fill the chip
+// with one thread per unit: a block takes kSplitUnits adjacent units (V
+// columns each) and splits their rows over kSplitSlices slices, thread
+// (slice s, unit g) taking rows s, s + kSplitSlices, ...  A row's eight units
+// are then 8 x 16 bytes side by side.  Per-slice maxima and sums meet in LDS
+// (the sums added in slice order); exp(x - max) / sum as the column kernel.
+constexpr uint32_t kSplitUnits = 8, kSplitSlices = kThreads / kSplitUnits;
+// Below this many units the split form is taken: one thread per unit would
+// give fewer than 256 blocks of kThreads.
+constexpr uint32_t kSplitMin = 256 * kThreads;
+template <typename TI, typename TO, int V, bool FAST>
+__global__ __launch_bounds__(kThreads) void softmax_col_split_kernel(SoftmaxPlan p) {
+  constexpr uint32_t C = kSplitUnits * V;  // columns of the block
+  __shared__ float part[kSplitSlices][C + 1];
+  __shared__ float col_max[C], col_sum[C];
+  const uint32_t g = threadIdx.x % kSplitUnits, sl = threadIdx.x / kSplitUnits;
+  const uint32_t unit = blockIdx.x * kSplitUnits + g;
+  const bool live = unit < p.units;
+  int64_t xo, oo;
+  col_offsets(p, min(unit, p.units - 1) * (uint32_t)V, xo, oo);
+  const TI* xc = static_cast<const TI*>(p.x) + xo;
+  TO* oc = static_cast<TO*>(p.out) + oo;
+  struct alignas(V * sizeof(TI) >= 16 ? 16 : alignof(TI)) WI { TI e[V]; };
+  struct alignas(V * sizeof(TO) >= 16 ? 16 : alignof(TO)) WO { TO e[V]; };
+  // one pass over the slice's rows, eight at a time: all eight loads
+  // (clamped into the column) issued before the first is used
+  constexpr uint32_t B = 8;
+  auto pass = [&](auto&& f) {
+    for (uint32_t r0 = sl; r0 < p.R; r0 += B * kSplitSlices) {
+      WI w[B];
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k)
+        w[k] = *reinterpret_cast<const WI*>(xc + (int64_t)min(r0 + k * kSplitSlices, p.R - 1) * p.xr);
+#pragma unroll
+      for (uint32_t k = 0; k < B; ++k)
+        if (r0 + k * kSplitSlices < p.R) f(r0 + k * kSplitSlices, w[k]);
+    }
+  };
+  float m[V], s[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    m[j] = -__builtin_inff();
+    s[j] = 0.f;
+  }
+  pass([&](uint32_t, const WI& w) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) m[j] = max_nan(m[j], (float)w.e[j]);
+  });
+#pragma unroll
+  for (int j = 0; j < V; ++j) part[sl][g * V + j] = m[j];
+  __syncthreads();
+  if (threadIdx.x < C) {
+    float t = part[0][threadIdx.x];
+    for (uint32_t q = 1; q < kSplitSlices; ++q) t = max_nan(t, part[q][threadIdx.x]);
+    col_max[threadIdx.x] = t;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < V; ++j) m[j] = col_max[g * V + j];
+  pass([&](uint32_t, const WI& w) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) s[j] += expd<FAST>((float)w.e[j], m[j]);
+  });
+#pragma unroll
+  for (int j = 0; j < V; ++j) part[sl][g * V + j] = s[j];
+  __syncthreads();
+  if (threadIdx.x < C) {
+    float t = 0.f;
+    for (uint32_t q = 0; q < kSplitSlices; ++q) t += part[q][threadIdx.x];
+    col_sum[threadIdx.x] = t;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < V; ++j) s[j] = col_sum[g * V + j];
+  if (!live) return;
+  pass([&](uint32_t r, const WI& w) {
+    WO o;
+#pragma unroll
+    for (int j = 0; j < V; ++j) o.e[j] = (TO)(expd<FAST>((float)w.e[j], m[j]) / s[j]);
+    *reinterpret_cast<WO*>(oc + (int64_t)r * p.orr) = o;
+  });
+}
+
 // Short fp16 column reductions (R <= 16 rows) over 16-byte column groups: the
 // DFL bin softmax over the [B,16,4,A] view (R = 16 rows at stride A).  A unit
 // is eight adjacent columns; SPLIT lanes share a unit, each holding 16/SPLIT
@@ -898,12 +981,22 @@ thin_status launch_softmax(const thin_desc* x, int dim, const thin_desc* out, hi
     hipLaunchKernelGGL((softmax_col_kernel<TI, TO, 2, 16, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
   } else if (vec) {
     p.units = (uint32_t)(cols / V);
-    const uint32_t grid = (p.units + kThreads - 1) / kThreads;
-    hipLaunchKernelGGL((softmax_col_kernel<TI, TO, V, 16, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
+    if (R > 16 && p.units < kSplitMin) {
+      const uint32_t grid = (p.units + kSplitUnits - 1) / kSplitUnits;
+      hipLaunchKernelGGL((softmax_col_split_kernel<TI, TO, V, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
+    } else {
+      const uint32_t grid = (p.units + kThreads - 1) / kThreads;
+      hipLaunchKernelGGL((softmax_col_kernel<TI, TO, V, 16, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
+    }
   } else {
     p.units = (uint32_t)cols;
-    const uint32_t grid = (p.units + kThreads - 1) / kThreads;
-    hipLaunchKernelGGL((softmax_col_kernel<TI, TO, 1, 32, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
+    if (R > 32 && p.units < kSplitMin) {
+      const uint32_t grid = (p.units + kSplitUnits - 1) / kSplitUnits;
+      hipLaunchKernelGGL((softmax_col_split_kernel<TI, TO, 1, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
+    } else {
+      const uint32_t grid = (p.units + kThreads - 1) / kThreads;
+      hipLaunchKernelGGL((softmax_col_kernel<TI, TO, 1, 32, FAST>), dim3(grid), dim3(kThreads), 0, stream, p);
+    }
   }
   THIN_LAUNCH_CHECK("softmax_col");
   return THIN_OK;
