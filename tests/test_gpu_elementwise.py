@@ -373,6 +373,37 @@ def test_errors_are_reported(gpu):
         capi.unary(capi.SILU, torch.ones(4, device=gpu, dtype=torch.int64))
 
 
+@pytest.mark.parametrize("dtype,shape", [(torch.float16, (4, 64, 48, 48)), (torch.float32, (2, 64, 48, 48))])
+def test_transposed_operand_first(gpu, dtype, shape):
+    """An operand that is a batched 2-D transpose of a dense output of 1 MB or
+    more goes through the tiled transpose into the output first.  The results
+    equal, bit for bit, the same op on a contiguous copy of that operand: as
+    either operand of every binary op (alpha 1 and 0.5), with a scalar, through
+    the unary ops and silu_add; and against the oracle.  An output that shares
+    bytes with an operand (x += y^T) keeps the direct path."""
+    from thintnpu_amd import capi
+    n, c, h, w = shape
+    bits = torch.int16 if dtype == torch.float16 else torch.int32
+    same = lambda a, b: torch.equal(a.cpu().view(bits), b.cpu().view(bits))  # noqa: E731
+    xt = torch.randn(n, h, w, c, generator=gen(7)).to(dtype).to(gpu).permute(0, 3, 1, 2)
+    xc = xt.contiguous()
+    y = (torch.randn(shape, generator=gen(8)).abs() + 0.5).to(dtype).to(gpu)
+    for op in range(4):
+        for alpha in ((1.0, 0.5) if op < 2 else (1.0,)):
+            got = capi.binary(op, xt, y, alpha)
+            assert same(got, capi.binary(op, xc, y, alpha)), f"op{op} a{alpha} x^T"
+            assert same(capi.binary(op, y, xt, alpha), capi.binary(op, y, xc, alpha)), f"op{op} a{alpha} y^T"
+            if dtype == torch.float16:
+                assert_ulp(got.cpu(), ew.binary(op, xt.cpu(), y.cpu(), alpha), 0, f"oracle op{op} a{alpha}")
+    for op in (capi.SIGMOID, capi.SILU):
+        assert same(capi.unary(op, xt), capi.unary(op, xc)), f"unary {op}"
+    assert same(capi.binary_scalar(2, xt, 0.3), capi.binary_scalar(2, xc, 0.3)), "scalar"
+    assert same(capi.silu_add(xt, y), capi.silu_add(xc, y)), "silu_add"
+    acc = y.clone()
+    capi.binary(0, acc, xt, 1.0, out=acc)
+    assert same(acc, capi.binary(0, y, xc, 1.0)), "in place"
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32, torch.int32, torch.bfloat16])
 def test_transpose_copy(gpu, dtype):
     """Batched 2-D transposes take the tiled path: full and partial tiles,

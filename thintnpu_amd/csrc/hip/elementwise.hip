@@ -1205,6 +1205,41 @@ thin_status copy_bits(const thin_desc* src, const thin_desc* dst, hipStream_t st
 
 using namespace thin;
 
+// Bytes [lo, hi) that a descriptor's elements span (strides are >= 0).
+void byte_span(const thin_desc* d, uintptr_t& lo, uintptr_t& hi) {
+  int64_t last = 0;
+  for (int i = 0; i < d->rank; ++i) last += (d->sizes[i] - 1) * d->strides[i];
+  lo = reinterpret_cast<uintptr_t>(d->data);
+  hi = lo + (uintptr_t)(last + 1) * (uintptr_t)dtype_size(d->dtype);
+}
+
+// An operand that is a batched 2-D transpose of a dense output (a permuted
+// view, x + y.transpose(1, 2)) would be gathered element by element, one
+// 2-byte read per lane: 75 us for [32,64,80,80] fp16 against 10.5 us for the
+// tiled transpose of the same tensor.  For outputs of 1 MB and more whose
+// bytes no operand shares, that operand is first transposed into the output
+// with the tiled kernel and the op then reads it there, in place (each
+// element read and written at one index by one thread).  The values, and so
+// the result's bits, are the same.  Returns the operand taken, or -1.
+constexpr int64_t kTransposeFirstBytes = 1 << 20;
+int transpose_operand_first(const thin_desc* out, const thin_desc* const* ins, int nin, hipStream_t stream) {
+  if (!is_contiguous(out) || numel(out) * dtype_size(out->dtype) < kTransposeFirstBytes) return -1;
+  uintptr_t olo, ohi;
+  byte_span(out, olo, ohi);
+  for (int k = 0; k < nin; ++k) {
+    uintptr_t lo, hi;
+    byte_span(ins[k], lo, hi);
+    if (lo < ohi && olo < hi) return -1;
+  }
+  for (int k = 0; k < nin; ++k) {
+    bool broadcast = false;  // stride-0 operands are read once per vector already
+    for (int i = 0; i < ins[k]->rank; ++i) broadcast |= ins[k]->sizes[i] > 1 && ins[k]->strides[i] == 0;
+    if (!broadcast && ins[k]->dtype == out->dtype && same_sizes(ins[k], out) && try_transpose(ins[k], out, stream))
+      return k;
+  }
+  return -1;
+}
+
 extern "C" thin_status thin_binary(int32_t op, const thin_desc* x, const thin_desc* y,
                                    const thin_desc* out, float alpha, hipStream_t stream) {
   clear_error();
@@ -1226,6 +1261,11 @@ extern "C" thin_status thin_binary(int32_t op, const thin_desc* x, const thin_de
     if (flat) {
       THIN_LAUNCH_CHECK("binary_channel_flat");
       return THIN_OK;
+    }
+    const int k = transpose_operand_first(out, ins, 2, stream);
+    if (k >= 0) {
+      THIN_LAUNCH_CHECK("binary_transpose_operand");
+      ins[k] = out;
     }
   }
   switch (op) {
@@ -1253,6 +1293,10 @@ extern "C" thin_status thin_binary_scalar(int32_t op, const thin_desc* x, double
   const bool additive = op == THIN_ADD || op == THIN_SUB;
   const float sv = additive ? round_to(out->dtype, scalar) : (float)scalar;
   alpha = round_to(out->dtype, alpha);
+  if (numel(out) != 0 && transpose_operand_first(out, ins, 1, stream) == 0) {
+    THIN_LAUNCH_CHECK("binary_scalar_transpose_operand");
+    ins[0] = out;
+  }
 #define THIN_SCALAR_CASE(OPC)                                                              \
   case OPC:                                                                                \
     return scalar_first ? dispatch_float<OpScalar<OPC, true>, 1>(out, ins, alpha, sv, stream) \
@@ -1276,6 +1320,10 @@ extern "C" thin_status thin_unary(int32_t op, const thin_desc* x, const thin_des
   thin_status s = check_float_operands("unary", all, 2);
   if (s) return s;
   const thin_desc* ins[1] = {x};
+  if (numel(out) != 0 && transpose_operand_first(out, ins, 1, stream) == 0) {
+    THIN_LAUNCH_CHECK("unary_transpose_operand");
+    ins[0] = out;
+  }
   switch (op) {
     case THIN_SIGMOID: return dispatch_float<OpSigmoid, 1>(out, ins, 0.f, 0.f, stream);
     case THIN_SILU: return dispatch_float<OpSilu, 1>(out, ins, 0.f, 0.f, stream);
@@ -1292,6 +1340,13 @@ extern "C" thin_status thin_silu_add(const thin_desc* x, const thin_desc* y, con
   thin_status s = check_float_operands("silu_add", all, 3);
   if (s) return s;
   const thin_desc* ins[2] = {x, y};
+  if (numel(out) != 0) {
+    const int k = transpose_operand_first(out, ins, 2, stream);
+    if (k >= 0) {
+      THIN_LAUNCH_CHECK("silu_add_transpose_operand");
+      ins[k] = out;
+    }
+  }
   return dispatch_float<OpSiluAdd, 2>(out, ins, 0.f, 0.f, stream);
 }
 
