@@ -44,6 +44,7 @@ constexpr uint32_t kStreamThreads = 256;
 // ============================================================ cat
 
 constexpr int kCatPerLaunch = 16;
+constexpr int64_t kCatShortRun = 512;  // bytes: shorter row runs copy through the strided path
 constexpr int kCatOuterDims = THIN_MAX_DIMS - 1;
 
 // One input of a cat launch: its fields lie together, so that a block reads
@@ -1238,7 +1239,11 @@ extern "C" thin_status thin_cat(const thin_desc* inputs, int32_t n, int32_t dim,
     const thin_desc* t = &inputs[k];
     const int64_t seg = t->sizes[dim];
     if (seg == 0 || numel(t) == 0) continue;
-    if (out_dense && run_dense(t, dim)) {
+    // a block per row run: runs under kCatShortRun would leave most of its
+    // lanes idle, so those inputs take the strided copy below, whose kernels
+    // pack many rows into a block (2 x [32,64,80,40] along the last dim, 80-byte
+    // runs: 333 us through blocks per run)
+    if (out_dense && run_dense(t, dim) && seg * inner * esize >= kCatShortRun) {
       bool vec = out_vec && aligned16(t->data) && (seg * inner * esize) % 16 == 0 && (col * inner * esize) % 16 == 0;
       for (int d = 0; vec && d < dim; ++d) vec = (t->strides[d] * esize) % 16 == 0 || t->sizes[d] == 1;
       if (vec) {
