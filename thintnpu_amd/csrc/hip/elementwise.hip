@@ -928,10 +928,51 @@ float round_to(int32_t dtype, double v) {
   return dtype == THIN_F16 ? (float)(_Float16)(float)v : (float)v;
 }
 
+// An elementwise op maps each element to itself, so any order of the dims
+// serves, applied to every operand alike.  The dims go in the order of the
+// output's strides, largest first (a stable sort): a permuted view written
+// into a view of the same permutation (channels-last memory seen as NCHW,
+// x.transpose(1, 2) into out.transpose(1, 2)) then coalesces into dense
+// runs instead of a gather along the view's inner dim.  Returns false when
+// the order already holds.
+bool order_by_output(const thin_desc* out, const thin_desc* const* ins, int nin, thin_desc& o2, thin_desc* i2) {
+  int perm[THIN_MAX_DIMS];
+  bool sorted = true;
+  for (int d = 0; d < out->rank; ++d) perm[d] = d;
+  for (int d = 1; d < out->rank; ++d) {
+    const int v = perm[d];
+    int j = d;
+    while (j > 0 && out->strides[perm[j - 1]] < out->strides[v]) {
+      perm[j] = perm[j - 1];
+      --j;
+      sorted = false;
+    }
+    perm[j] = v;
+  }
+  if (sorted) return false;
+  auto apply = [&](const thin_desc* src, thin_desc& dst) {
+    dst = *src;
+    for (int d = 0; d < src->rank; ++d) {
+      dst.sizes[d] = src->sizes[perm[d]];
+      dst.strides[d] = src->strides[perm[d]];
+    }
+  };
+  apply(out, o2);
+  for (int k = 0; k < nin; ++k) apply(ins[k], i2[k]);
+  return true;
+}
+
 template <class Op, int NIN>
 thin_status dispatch_float(const thin_desc* out, const thin_desc* const* ins, float pa, float pb,
                            hipStream_t stream) {
   if (numel(out) == 0) return THIN_OK;
+  thin_desc o2, i2[NIN];
+  const thin_desc* ip[NIN];
+  if (order_by_output(out, ins, NIN, o2, i2)) {
+    for (int k = 0; k < NIN; ++k) ip[k] = &i2[k];
+    out = &o2;
+    ins = ip;
+  }
   if (out->dtype == THIN_F16) return launch_map<_Float16, NIN, Op>(out, ins, pa, pb, stream);
   return launch_map<float, NIN, Op>(out, ins, pa, pb, stream);
 }
