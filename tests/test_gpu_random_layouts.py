@@ -163,3 +163,29 @@ def test_softmax_random_views(gpu, half_to_float):
         xc, xg = random_view(rng, shape, torch.float16, gpu, 5 * case + 11)
         got = capi.softmax(xg, dim, half_to_float).cpu()
         check_softmax(got, xc, dim, half_to_float, f"case {case} dim {dim} {shape}/{list(xc.stride())}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_channels_last_views(gpu, dtype):
+    """Operands and outputs that are NCHW views of NHWC memory (the dims go
+    in the output's stride order before coalescing), with a per-channel
+    operand and a contiguous operand among them, against the oracle."""
+    from thintnpu_amd import capi
+    n, c, h, w = 2, 48, 9, 13
+    cl = lambda seed: torch.randn(n, h, w, c, generator=gen(seed)).to(dtype)  # noqa: E731
+    xh, yh = cl(1).permute(0, 3, 1, 2), (cl(2).abs() + 0.5).permute(0, 3, 1, 2)
+    bias = torch.randn(1, c, 1, 1, generator=gen(3)).to(dtype)
+    dense = torch.randn(n, c, h, w, generator=gen(4)).to(dtype)
+    xg, yg, bg, dg = (t.to(gpu) for t in (xh, yh, bias, dense))
+    for op in range(4):
+        for (a, b), (ag, bg2) in (((xh, yh), (xg, yg)), ((xh, bias), (xg, bg)), ((dense, xh), (dg, xg))):
+            out = torch.empty(n, h, w, c, dtype=dtype, device=gpu).permute(0, 3, 1, 2)
+            capi.binary(op, ag, bg2, 1.0, out=out)
+            check(out.cpu(), ew.binary(op, a, b, 1.0), f"op{op} {list(a.stride())} {list(b.stride())}")
+    for op, ref in ((capi.SIGMOID, ew.sigmoid), (capi.SILU, ew.silu)):
+        out = torch.empty(n, h, w, c, dtype=dtype, device=gpu).permute(0, 3, 1, 2)
+        capi.unary(op, xg, out=out)
+        if dtype == torch.float16:
+            assert_ulp(out.cpu(), ref(xh), 2, f"unary {op}")
+        else:
+            torch.testing.assert_close(out.cpu(), ref(xh), rtol=1e-5, atol=1e-6)
