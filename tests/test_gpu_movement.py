@@ -181,6 +181,14 @@ def test_upsample_nchw(gpu, dtype):
     x = rand_dtype((2, 14, 15, 17), dtype, 3)
     sec = x[:, 7:]
     assert bits_equal(capi.upsample2x_nchw(x.to(gpu)[:, 7:]).cpu(), mv.upsample2x_nchw(sec))
+    # rows the 16-byte form cannot take: odd widths, stepped and transposed inputs
+    x = rand_dtype((3, 8, 41, 37), dtype, 6)
+    assert bits_equal(capi.upsample2x_nchw(x.to(gpu)).cpu(), mv.upsample2x_nchw(x)), "41x37"
+    x = rand_dtype((2, 5, 9, 22), dtype, 4)
+    assert bits_equal(capi.upsample2x_nchw(x.to(gpu)[..., ::2]).cpu(), mv.upsample2x_nchw(x[..., ::2])), "stepped"
+    x = rand_dtype((2, 5, 11, 9), dtype, 5)
+    got = capi.upsample2x_nchw(x.to(gpu).transpose(2, 3)).cpu()
+    assert bits_equal(got, mv.upsample2x_nchw(x.transpose(2, 3))), "transposed"
 
 
 def test_pack_unpack(gpu):

@@ -477,6 +477,35 @@ __global__ __launch_bounds__(kThreads) void nchw_up_kernel(NchwUpPlan p) {
   }
 }
 
+// NCHW 2x upsample for rows the 16-byte form cannot take (odd or unaligned
+// output widths, gapped or strided input rows): a thread per input element
+// stores it to its two output rows as one two-element word each (columns 2x
+// and 2x + 1), so a wave writes 2 x 64 words side by side.
+struct NchwPairPlan {
+  const char* src;
+  char* dst;
+  int64_t s_n, s_c, s_h, s_w;  // input strides (bytes)
+  int64_t d_n, d_c, d_h;       // output strides (bytes); w dense
+  uint32_t w, h, c, total;     // input width, height, channels; N * C * H * W
+  FastDiv div_w, div_h, div_c;
+};
+
+template <typename E, typename E2>
+__global__ __launch_bounds__(kThreads) void nchw_up_pair_kernel(NchwPairPlan p) {
+  for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < p.total; e += gridDim.x * kThreads) {
+    const uint32_t r = p.div_w.div(e), x = e - r * p.w;
+    const uint32_t nc = p.div_h.div(r), y = r - nc * p.h;
+    const uint32_t n = p.div_c.div(nc), c = nc - n * p.c;
+    const E v = *reinterpret_cast<const E*>(p.src + n * p.s_n + c * p.s_c + (int64_t)y * p.s_h + (int64_t)x * p.s_w);
+    E2 pair;
+    pair[0] = v;
+    pair[1] = v;
+    char* d = p.dst + n * p.d_n + c * p.d_c + (int64_t)(2 * y) * p.d_h + (int64_t)x * (int64_t)sizeof(E2);
+    *reinterpret_cast<E2*>(d) = pair;
+    *reinterpret_cast<E2*>(d + p.d_h) = pair;
+  }
+}
+
 // ============================================================ max pool
 // Stride-1 max pool with an odd k x k window and "same" padding (taps outside
 // the plane are skipped, i.e. -inf).  A thread owns one pixel vector (V
@@ -1326,6 +1355,32 @@ extern "C" thin_status thin_upsample2x_nchw(const thin_desc* x, const thin_desc*
                    reinterpret_cast<uintptr_t>(x->data) % 8 == 0 && (x->strides[0] * esize) % 8 == 0 &&
                    (x->strides[1] * esize) % 8 == 0 && (x->strides[2] * esize) % 8 == 0;
   const uint64_t rows = (uint64_t)y->sizes[0] * y->sizes[1] * y->sizes[2];
+  const uint64_t in_elems = (uint64_t)numel(x);
+  const bool pair = (esize == 2 || esize == 4) && y->strides[3] == 1 && y->strides[0] % 2 == 0 &&
+                    y->strides[1] % 2 == 0 && y->strides[2] % 2 == 0 &&
+                    reinterpret_cast<uintptr_t>(y->data) % (2 * esize) == 0 && in_elems < (1ull << 31);
+  if (!vec && pair) {
+    NchwPairPlan p;
+    p.src = static_cast<const char*>(x->data);
+    p.dst = static_cast<char*>(y->data);
+    p.s_n = x->strides[0] * esize; p.s_c = x->strides[1] * esize;
+    p.s_h = x->strides[2] * esize; p.s_w = x->strides[3] * esize;
+    p.d_n = y->strides[0] * esize; p.d_c = y->strides[1] * esize; p.d_h = y->strides[2] * esize;
+    p.w = (uint32_t)x->sizes[3];
+    p.h = (uint32_t)x->sizes[2];
+    p.c = (uint32_t)x->sizes[1];
+    p.total = (uint32_t)in_elems;
+    p.div_w = FastDiv::make(p.w);
+    p.div_h = FastDiv::make(p.h);
+    p.div_c = FastDiv::make(p.c);
+    const uint32_t grid = grid_for(in_elems, kThreads, 1, 256u * 16u);
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    if (esize == 2) hipLaunchKernelGGL((nchw_up_pair_kernel<uint16_t, u16x2>), dim3(grid), dim3(kThreads), 0, stream, p);
+    else hipLaunchKernelGGL((nchw_up_pair_kernel<uint32_t, u32x2>), dim3(grid), dim3(kThreads), 0, stream, p);
+    THIN_LAUNCH_CHECK("upsample2x_nchw_pairs");
+    return THIN_OK;
+  }
   if (!vec || rows * (uint64_t)(ow * esize / 16) >= (1ull << 31)) {
     thin_desc x5 = *x, y5 = *y;
     x5.rank = y5.rank = 5;
