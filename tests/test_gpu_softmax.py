@@ -185,10 +185,15 @@ def test_dfl_expect_views_and_specials(gpu):
         y[1, 32, 12], y[1, 47, 12] = 65504.0, -65504.0  # fp16 extremes in one side
         y[1, 48:64, 13] = float("-inf")
         y[1, 50, 13] = 1.0                            # one finite bin: expectation 2
+        # the same values anchor-major (each anchor's 64 bins contiguous)
+        ya = y.transpose(1, 2).contiguous().transpose(1, 2)
         for out_dtype in (torch.float16, torch.float32):
             got = capi.dfl_expect(y.to(gpu), out_dtype).cpu()
             assert_rel(got, rd.dfl_expect(y, out_dtype), 1e-3, f"dfl specials {width} {out_dtype}")
+            got = capi.dfl_expect(ya.to(gpu).transpose(1, 2).contiguous().transpose(1, 2), out_dtype).cpu()
+            assert_rel(got, rd.dfl_expect(ya, out_dtype), 1e-3, f"dfl anchor-major specials {width} {out_dtype}")
         assert float(capi.dfl_expect(y.to(gpu)).cpu()[1, 3, 13]) == 2.0
+        assert float(capi.dfl_expect(y.to(gpu).transpose(1, 2).contiguous().transpose(1, 2)).cpu()[1, 3, 13]) == 2.0
 
 
 @pytest.mark.parametrize("n", [1, 32])

@@ -628,6 +628,31 @@ __global__ __launch_bounds__(kThreads) void dfl_expect_kernel(DflPlan p) {
   }
 }
 
+// Anchor-major logits (bin stride 1, anchor rows of 64 bins, the layout of
+// a channels-last head seen as [N,64,A]): a thread per (anchor, side), side
+// fastest, reads its 16 bins as two 16-byte loads, so four threads read an
+// anchor's 128 bytes together; units = N * A * 4, div_avecs divides by A.
+// The math is dev::dfl_side<1> (the one-anchor form's bits).
+template <typename TO, bool FAST>
+__global__ __launch_bounds__(kThreads) void dfl_expect_rows_kernel(DflPlan p) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const uint32_t u0 = blockIdx.x * kThreads + threadIdx.x, u = min(u0, p.units - 1);
+  const uint32_t sd = u & 3u, rest = u >> 2;
+  const uint32_t n = p.div_avecs.div(rest), a = rest - n * p.avecs;
+  const _Float16* src = p.x + (int64_t)n * p.xn + (int64_t)a * p.xa + sd * 16u;
+  const h8 lo = *reinterpret_cast<const h8*>(src), hi = *reinterpret_cast<const h8*>(src + 8);
+  _Float16 bins[16][1];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    bins[i][0] = lo[i];
+    bins[8 + i][0] = hi[i];
+  }
+  float r[1];
+  dev::dfl_side<1, FAST>(bins, r);
+  if (u0 >= p.units) return;
+  static_cast<TO*>(p.out)[(int64_t)n * p.on + (int64_t)sd * p.os + (int64_t)a * p.oa] = (TO)r[0];
+}
+
 // ---------------------------------------------------------------- detect decode
 // Anchor-free detect head in one launch (whole_blocked.py:118-146):
 //   distance = DFL(boxes)                      [B,4,A] fp16 (dev::dfl_side)
@@ -1040,6 +1065,23 @@ extern "C" thin_status thin_dfl_expect(const thin_desc* x, const thin_desc* out,
   const int64_t A = x->sizes[2];
   p.sides = (uint32_t)(x->sizes[0] * 4);
   const int esz = out->dtype == THIN_F32 ? 4 : 2;
+  if (p.xc == 1 && p.xa % 8 == 0 && p.xn % 8 == 0 && aligned(x->data, 16) && p.xa >= 64) {
+    // anchor-major bins: 16 -> 2 load instructions per (anchor, side) and
+    // whole 128-byte anchor rows per four lanes ([32,64,8400] as the
+    // transpose of [32,8400,64]: 111.6 us through the strided form)
+    const uint64_t units = (uint64_t)p.sides * (uint64_t)A;
+    THIN_REQUIRE(units < (1ull << 31), THIN_ERR_UNSUPPORTED, "dfl_expect: tensor too large");
+    p.units = (uint32_t)units;
+    p.avecs = (uint32_t)A;
+    p.div_avecs = FastDiv::make(p.avecs);
+    const uint32_t grid = (p.units + kThreads - 1) / kThreads;
+    if (out->dtype == THIN_F16)
+      hipLaunchKernelGGL((dfl_expect_rows_kernel<_Float16, true>), dim3(grid), dim3(kThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((dfl_expect_rows_kernel<float, false>), dim3(grid), dim3(kThreads), 0, stream, p);
+    THIN_LAUNCH_CHECK("dfl_expect_rows");
+    return THIN_OK;
+  }
   // Two anchors per thread (4-byte loads): more waves than wider vectors, so
   // the 32 exponentials per thread overlap the loads of other waves.
   constexpr int V = 2;
