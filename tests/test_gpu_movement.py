@@ -204,6 +204,12 @@ def test_pack_unpack(gpu):
     x = random_bits16((2, 32, 12, 10), 4)
     xt = x.transpose(2, 3)
     assert bits_equal(capi.pack_nc1hwc0(x.to(gpu).transpose(2, 3)).cpu(), mv.pack_blocked(xt))
+    # channels-last x (NHWC memory seen as NCHW), packed and unpacked back into one
+    cl = random_bits16((3, 11, 7, 48), 9).permute(0, 3, 1, 2)
+    yc = capi.pack_nc1hwc0(cl.to(gpu))
+    assert bits_equal(yc.cpu(), mv.pack_blocked(cl)), "channels-last pack"
+    out = torch.empty(3, 11, 7, 48, dtype=torch.float16, device=gpu).permute(0, 3, 1, 2)
+    assert bits_equal(capi.unpack_nc1hwc0(yc, 48, out=out).cpu(), cl), "channels-last unpack"
 
 
 def test_movement_errors(gpu):

@@ -1147,10 +1147,16 @@ thin_status repack(const thin_desc* nchw, const thin_desc* blocked, bool to_bloc
                       blocked->strides[1] % 8 == 0;
   int64_t hw_stride = 0;
   const bool pix = pixels_axis(nchw, hw_stride);
-  if (!bdense || !pix) {
-    // general strides: element-wise index map through the 5-D view of NCHW
-    // (x[n, c1*16+k, h, w] <-> y[n, c1, h, w, k]); channels >= C of a pack
-    // must read as zero, which the index map cannot express, so require C%16.
+  // channels-last NCHW (channel stride 1): the tiled kernel below reads
+  // pixels along its lanes, which there lie C elements apart
+  const bool chan_last = nchw->strides[1] == 1 && c > 1 && c % 16 == 0;
+  if (!bdense || !pix || chan_last) {
+    // general strides: the strided copy through the 5-D view of NCHW
+    // (x[n, c1*16+k, h, w] <-> y[n, c1, h, w, k]), whose kernels coalesce and
+    // vectorise what the layouts share (a channels-last x moves 32-byte C0
+    // runs: [32,64,80,80] 205 us through an element-wise index map); channels
+    // >= C of a pack must read as zero, which a view cannot express, so
+    // require C % 16.
     THIN_REQUIRE(c % 16 == 0 || !to_blocked, THIN_ERR_UNSUPPORTED,
                  "pack: non-dense layouts need C %% 16 == 0");
     thin_desc v5 = *nchw;
@@ -1161,10 +1167,10 @@ thin_status repack(const thin_desc* nchw, const thin_desc* blocked, bool to_bloc
     v5.sizes[2] = h; v5.strides[2] = nchw->strides[2];
     v5.sizes[3] = w; v5.strides[3] = nchw->strides[3];
     v5.sizes[4] = 16; v5.strides[4] = cs;
-    if (to_blocked) return launch_up5(&v5, blocked, false, stream);
+    if (to_blocked) return copy_bits(&v5, blocked, stream);
     // unpack of the first C channels only
     thin_desc b5 = *blocked;
-    if (c % 16 == 0) return launch_up5(blocked, &v5, false, stream);
+    if (c % 16 == 0) return copy_bits(blocked, &v5, stream);
     // partial last block: full blocks, then the tail channels
     THIN_REQUIRE(false, THIN_ERR_UNSUPPORTED, "unpack: non-dense layout with C %% 16 != 0");
     (void)b5;
