@@ -994,13 +994,30 @@ struct FillPlan {
   int64_t stride[kMaxDims];  // elements
   uint64_t total;
   uint64_t bits;
+  FastDiv div[kMaxDims];     // of size[], for SMALL launches (total < 2^31)
 };
 
-template <typename T>
+// SMALL: fewer than 2^31 elements, so the index splits with 32-bit FastDiv
+// steps instead of 64-bit divisions (a stride-2 fp16 view of [32,64,80,160]:
+// 21.1 -> 17.7 us).
+template <typename T, bool SMALL>
 __global__ __launch_bounds__(kThreads) void fill_strided_kernel(FillPlan p) {
   const T v = __builtin_bit_cast(T, (typename std::conditional<sizeof(T) == 8, uint64_t,
                                      typename std::conditional<sizeof(T) == 4, uint32_t,
                                      typename std::conditional<sizeof(T) == 2, uint16_t, uint8_t>::type>::type>::type)p.bits);
+  if constexpr (SMALL) {
+    for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < (uint32_t)p.total; e += gridDim.x * kThreads) {
+      uint32_t rest = e;
+      int64_t off = 0;
+      for (int d = 0; d < p.nd; ++d) {
+        const uint32_t q = p.div[d].div(rest);
+        off += (int64_t)(rest - q * p.div[d].d) * p.stride[d];
+        rest = q;
+      }
+      reinterpret_cast<T*>(p.out)[off] = v;
+    }
+    return;
+  }
   for (uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x; e < p.total; e += (uint64_t)gridDim.x * kThreads) {
     uint64_t rest = e;
     int64_t off = 0;
@@ -1455,13 +1472,22 @@ extern "C" thin_status thin_fill(const thin_desc* out, double value, int64_t iva
   }
   p.total = (uint64_t)total;
   p.bits = bits;
+  const bool small = (uint64_t)total < (1ull << 31);
+  if (small)
+    for (int i = 0; i < c.nd; ++i) p.div[i] = FastDiv::make((uint32_t)p.size[i]);
   const uint32_t grid = grid_for((uint64_t)total, kThreads, 1, 65536u);
+#define THIN_FILL(T)                                                                                          \
+  do {                                                                                                        \
+    if (small) hipLaunchKernelGGL((fill_strided_kernel<T, true>), dim3(grid), dim3(kThreads), 0, stream, p);  \
+    else hipLaunchKernelGGL((fill_strided_kernel<T, false>), dim3(grid), dim3(kThreads), 0, stream, p);       \
+  } while (0)
   switch (esz) {
-    case 1: hipLaunchKernelGGL(fill_strided_kernel<uint8_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL(fill_strided_kernel<uint16_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
-    case 4: hipLaunchKernelGGL(fill_strided_kernel<uint32_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
-    default: hipLaunchKernelGGL(fill_strided_kernel<uint64_t>, dim3(grid), dim3(kThreads), 0, stream, p); break;
+    case 1: THIN_FILL(uint8_t); break;
+    case 2: THIN_FILL(uint16_t); break;
+    case 4: THIN_FILL(uint32_t); break;
+    default: THIN_FILL(uint64_t); break;
   }
+#undef THIN_FILL
   THIN_LAUNCH_CHECK("fill");
   return THIN_OK;
 }
